@@ -1,0 +1,256 @@
+"""Benchmark of the INT8 linear-layer hot path on one MI355X.
+
+Metric: INT8 TOPS and % of dense INT8 MFMA peak for fused_channel_mm at
+M=4096, K=5120, N=17408. One step is the prefill-projection pass of configs[2]:
+quantize_rows on BF16 [4096, 5120] (N(0,1), 0.1% of channels x50) followed by
+fused_channel_mm against signed INT8 weights [17408, 5120] with BF16 channel scales.
+`value` is 2*M*N*K / (wall time per step), i.e. the quantizer's time is charged to the
+GEMM. Inputs are resident in HBM before timing; the weights, activations and codes
+rotate over enough copies that no step finds its inputs in the 256 MB Infinity Cache.
+
+Also reported: `roofline` for the dominant kernel (the GEMM, timed per launch with HIP
+events on the stream it runs on), the quantizer and the W8A16 GEMV as
+extra roofline lines, and `cpu_baseline`, the CPU oracle on a bounded row slice of the
+same workload on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-extras]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "consumer-int8-kernels_amd"))
+sys.path.insert(0, str(REPO))
+
+M, K, N = 4096, 5120, 17408
+GEMM_OPS = 2 * M * N * K  # 730,144,440,320
+QUANT_BYTES = 3 * M * K + 4 * M  # BF16 read + INT8 write + FP32 scales
+PEAK_INT8_TOPS = 256 * 2.4e9 * 8192 / 1e12  # 5033.2: 256 CUs x 2.4 GHz x 8192 op/clk/CU
+PEAK_HBM_GBS = 8000.0
+GEMV_K, GEMV_N = 5120, 17408
+
+
+def gemv_bytes(m: int) -> int:
+    return GEMV_N * GEMV_K + 2 * GEMV_N + 2 * m * GEMV_K + 2 * m * GEMV_N
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=30)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extras", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="approximate CPU time budget of the cpu_baseline sample")
+    return p.parse_args()
+
+
+def make_inputs(torch, gen, copies_w=3, copies_x=3):
+    dev = "cuda"
+    xs = []
+    for _ in range(copies_x):
+        x = torch.randn(M, K, generator=gen, device=dev, dtype=torch.float32)
+        cols = torch.randperm(K, generator=gen, device=dev)[: max(1, K // 1000)]
+        x[:, cols] *= 50
+        xs.append(x.to(torch.bfloat16))
+    ws = [torch.randint(-127, 128, (N, K), generator=gen, device=dev, dtype=torch.int8)
+          for _ in range(copies_w)]
+    sw = (torch.rand(N, generator=gen, device=dev) * 9e-3 + 1e-3).to(torch.bfloat16)
+    codes = [torch.empty(M, K, device=dev, dtype=torch.int8) for _ in range(copies_x)]
+    sa = torch.empty(M, device=dev, dtype=torch.float32)
+    out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    return xs, ws, sw, codes, sa, out
+
+
+def time_kernel(torch, calls, reps):
+    """Mean and median per-launch time (us) of a rotating list of launch closures,
+    each bracketed by HIP events on the current stream."""
+    events = []
+    for i in range(reps):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        calls[i % len(calls)]()
+        end.record()
+        events.append((start, end))
+    torch.cuda.synchronize()
+    times = [s.elapsed_time(e) * 1e3 for s, e in events]
+    return statistics.mean(times), statistics.median(times)
+
+
+def cpu_baseline(budget_s: float) -> dict:
+    """The CPU oracle (numpy, float64-exact integer GEMM) on a row slice of the step."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+    except Exception:  # pragma: no cover - threadpoolctl is optional
+        threads = os.cpu_count() or 1
+    rng = np.random.default_rng(0)
+    w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    sw = O.f32_to_bf16(rng.uniform(1e-3, 1e-2, N).astype(np.float32))
+
+    def run(rows):
+        x = rng.standard_normal((rows, K)).astype(np.float32)
+        x[:, :5] *= 50
+        x_bits = O.f32_to_bf16(x)
+        t0 = time.perf_counter()
+        codes, sa = O.quantize_rows(x_bits)
+        O.fused_channel_mm(codes, w, sa, sw)
+        return time.perf_counter() - t0
+
+    rows = 64
+    elapsed = run(rows)
+    rows = int(min(M, max(64, rows * budget_s / max(elapsed, 1e-3))))
+    elapsed = run(rows)
+    tops = 2 * rows * N * K / elapsed / 1e12
+    return {
+        "value": round(tops, 4),
+        "unit": "TOPS",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"oracle quantize_rows + fused_channel_mm on {rows} of {M} rows "
+                  f"(K={K}, N={N}), {elapsed:.2f} s; CPU {platform.processor() or platform.machine()}",
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (--gpus {args.gpus} requested): this build has "
+              "no multi-GPU path; see DESIGN.md for how the op would shard.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from consumer_int8 import ops
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    props = torch.cuda.get_device_properties(0)
+    cus = props.multi_processor_count
+    peak_tops = PEAK_INT8_TOPS * cus / 256
+    gen = torch.Generator(device="cuda").manual_seed(20261011)
+    xs, ws, sw, codes, sa, out = make_inputs(torch, gen)
+
+    def step(i):
+        x, c, w = xs[i % len(xs)], codes[i % len(codes)], ws[i % len(ws)]
+        ops.quantize_rows(x, c, sa)
+        ops.fused_channel_mm(c, w, sa, sw, out, 0)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # Timed region: exactly K steps between synchronizations; GEMM launches bracketed by
+    # events on the current stream (the stream the ops launch on).
+    gemm_events = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        x, c, w = xs[i % len(xs)], codes[i % len(codes)], ws[i % len(ws)]
+        ops.quantize_rows(x, c, sa)
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        ops.fused_channel_mm(c, w, sa, sw, out, 0)
+        end.record()
+        gemm_events.append((start, end))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+    gemm_us = [s.elapsed_time(e) * 1e3 for s, e in gemm_events]
+    gemm_mean_us = statistics.mean(gemm_us)
+    gemm_tops = GEMM_OPS / (gemm_mean_us * 1e-6) / 1e12
+    value = GEMM_OPS / (ms_per_step * 1e-3) / 1e12
+
+    result = {
+        "metric": "INT8 TOPS + %MFMA peak, fused_channel_mm M=4096 K=5120 N=17408",
+        "value": round(value, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded on device): x BF16 N(0,1) with 0.1% channels x50, "
+                "w INT8 U[-127,127], w_scale BF16 U[1e-3,1e-2]",
+        "config": {"workload": "configs[2] prefill projection: quantize_rows BF16[4096,5120] "
+                               "+ fused_channel_mm M=4096 K=5120 N=17408",
+                   "M": M, "K": K, "N": N, "schedule": 0},
+        "pct_mfma_peak": round(100 * value / peak_tops, 2),
+        "roofline": {
+            "kernel": "fused_channel_mm",
+            "bound": "mfma",
+            "achieved": round(gemm_tops, 2),
+            "peak": round(peak_tops, 1),
+            "unit": "TFLOP/s",
+            "frac": round(gemm_tops / peak_tops, 4),
+            "traffic": None,
+            "mean_us": round(gemm_mean_us, 2),
+            "median_us": round(statistics.median(gemm_us), 2),
+            "ops_per_launch": GEMM_OPS,
+        },
+        "device": {"name": props.name, "cus": cus, "gcn_arch": getattr(props, "gcnArchName", "")},
+    }
+
+    if not args.no_extras:
+        extras = {}
+        # quantize_rows [4096, 5120]: rotate 5 (x, codes) pairs = 315 MB > MALL.
+        qx = [torch.randn(M, K, generator=gen, device="cuda").to(torch.bfloat16) for _ in range(5)]
+        qc = [torch.empty(M, K, device="cuda", dtype=torch.int8) for _ in range(5)]
+        calls = [lambda i=i: ops.quantize_rows(qx[i], qc[i], sa) for i in range(5)]
+        for c in calls:
+            c()
+        mean_us, med_us = time_kernel(torch, calls, 50)
+        gbs = QUANT_BYTES / (mean_us * 1e-6) / 1e9
+        extras["quantize_rows"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                                   "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                   "mean_us": round(mean_us, 2), "bytes": QUANT_BYTES}
+        del qx, qc
+        # channel_gemv K=5120, N=17408: rotate 4 weight copies = 356 MB > MALL.
+        gw = [torch.randint(-127, 128, (GEMV_N, GEMV_K), generator=gen, device="cuda",
+                            dtype=torch.int8) for _ in range(4)]
+        gs = (torch.rand(GEMV_N, generator=gen, device="cuda") * 9e-3 + 1e-3).to(torch.bfloat16)
+        for m in (1, 4, 8, 16):
+            gx = torch.randn(m, GEMV_K, generator=gen, device="cuda").to(torch.bfloat16)
+            go = torch.empty(m, GEMV_N, device="cuda", dtype=torch.bfloat16)
+            calls = [lambda i=i: ops.channel_gemv(gx, gw[i], gs, go) for i in range(4)]
+            for c in calls:
+                c()
+            mean_us, med_us = time_kernel(torch, calls, 40)
+            gbs = gemv_bytes(m) / (mean_us * 1e-6) / 1e9
+            extras[f"channel_gemv_m{m}"] = {"bound": "hbm", "achieved": round(gbs, 1),
+                                            "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                            "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                            "mean_us": round(mean_us, 2), "bytes": gemv_bytes(m)}
+        result["extras"] = extras
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,144 @@
+// The C ABI (include/consumer_int8_amd.h): argument validation, then the launch.
+//
+// Validation is pure host code and runs before any HIP call, so every rejection can be
+// exercised on a machine without a GPU. Messages reuse the reference's wording
+// (csrc/bindings.cpp) so callers matching on it keep working.
+#include "consumer_int8_amd.h"
+
+#include <climits>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "launch.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* message) {
+  g_last_error = message;
+  return status;
+}
+
+int launched(hipError_t error) {
+  if (error != hipSuccess) {
+    g_last_error = std::string("HIP launch failed: ") + hipGetErrorString(error);
+    return CI8_ERR_LAUNCH;
+  }
+  g_last_error.clear();
+  return CI8_OK;
+}
+
+bool aligned(const void* p, uintptr_t bytes) {
+  return reinterpret_cast<uintptr_t>(p) % bytes == 0;
+}
+
+bool overlap(const void* a, int64_t bytes_a, const void* b, int64_t bytes_b) {
+  const auto first = reinterpret_cast<uintptr_t>(a);
+  const auto second = reinterpret_cast<uintptr_t>(b);
+  return bytes_a > 0 && bytes_b > 0 && first < second + uint64_t(bytes_b) &&
+         second < first + uint64_t(bytes_a);
+}
+
+hipStream_t as_stream(void* stream) { return static_cast<hipStream_t>(stream); }
+
+// Shared GEMM geometry (csrc/bindings.cpp:402-408 for the signed ops,
+// csrc/bindings.cpp:252-258 for channel_mm).
+int check_gemm(int64_t m, int64_t n, int64_t k, bool need_n4, const char* what) {
+  if (!(m > 0 && n > 0 && k > 0 && k % 32 == 0 && k <= 65536 && (!need_n4 || n % 4 == 0)))
+    return fail(CI8_ERR_GEOMETRY, what);
+  if (m * k > INT_MAX || n * k > INT_MAX || m * n > INT_MAX)
+    return fail(CI8_ERR_TOO_LARGE, "Matrix too large");
+  return CI8_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ci8_last_error(void) { return g_last_error.c_str(); }
+
+const char* ci8_version(void) { return "0.1.0"; }
+
+int ci8_quantize_rows(const void* x, int8_t* codes, float* scales, int64_t m, int64_t k,
+                      void* stream) {
+  if (!(m > 0 && k > 0)) return fail(CI8_ERR_GEOMETRY, "Expected a nonempty BF16 matrix");
+  if (m * k > INT_MAX) return fail(CI8_ERR_TOO_LARGE, "Matrix too large");
+  if (!aligned(x, 2) || !aligned(scales, 4))
+    return fail(CI8_ERR_ALIGNMENT, "quantize_rows requires aligned buffers");
+  return launched(ci8::launch_quantize_rows(x, codes, scales, int(m), int(k), as_stream(stream)));
+}
+
+int ci8_quantize_grouped4096(const void* x, int8_t* codes, float* scales, int64_t m,
+                             int64_t groups, void* stream) {
+  constexpr int64_t kWidth = 4096;
+  if (!(m >= 0 && groups > 0))
+    return fail(CI8_ERR_GEOMETRY,
+                "Expected BF16 input[M,G,4096], INT8 codes[G,M,4096], FP32 scales[G,M]");
+  if (m * groups * kWidth > INT_MAX)
+    return fail(CI8_ERR_GEOMETRY,
+                "Expected BF16 input[M,G,4096], INT8 codes[G,M,4096], FP32 scales[G,M]");
+  if (!aligned(x, 16) || !aligned(codes, 8) || !aligned(scales, 4))
+    return fail(CI8_ERR_ALIGNMENT, "Grouped quantization requires aligned buffers");
+  const int64_t elems = m * groups * kWidth;
+  if (overlap(x, elems * 2, codes, elems) || overlap(x, elems * 2, scales, m * groups * 4) ||
+      overlap(codes, elems, scales, m * groups * 4))
+    return fail(CI8_ERR_OVERLAP, "Grouped quantization buffers must not overlap");
+  return launched(ci8::launch_quantize_grouped(x, codes, scales, int(m), int(groups),
+                                               int(kWidth), as_stream(stream)));
+}
+
+int ci8_fused_channel_mm(const int8_t* a, const int8_t* w, const float* a_scale,
+                         const void* w_scale, void* out, int64_t m, int64_t n, int64_t k,
+                         int64_t schedule, void* stream) {
+  if (int s = check_gemm(m, n, k, true, "Invalid CUTLASS geometry")) return s;
+  if (!(schedule >= 0 && schedule <= 6))
+    return fail(CI8_ERR_SCHEDULE, "Invalid fused GEMM schedule");
+  if (!aligned(a, 16) || !aligned(w, 16) || !aligned(a_scale, 4) || !aligned(w_scale, 2) ||
+      !aligned(out, 2))
+    return fail(CI8_ERR_ALIGNMENT, "fused_channel_mm requires aligned buffers");
+  return launched(ci8::launch_channel_gemm(a, w, ci8::WeightCode::kSigned, a_scale, w_scale,
+                                           out, nullptr, int(m), int(n), int(k), int(schedule),
+                                           as_stream(stream)));
+}
+
+int ci8_cutlass_channel_mm(const int8_t* a, const int8_t* w, const float* a_scale,
+                           const void* w_scale, int32_t* workspace, void* out, int64_t m,
+                           int64_t n, int64_t k, void* stream) {
+  if (int s = check_gemm(m, n, k, true, "Invalid CUTLASS geometry")) return s;
+  if (!aligned(a, 16) || !aligned(w, 16) || !aligned(a_scale, 4) || !aligned(w_scale, 2) ||
+      !aligned(out, 2) || !aligned(workspace, 4))
+    return fail(CI8_ERR_ALIGNMENT, "cutlass_channel_mm requires aligned buffers");
+  return launched(ci8::launch_channel_gemm(a, w, ci8::WeightCode::kSigned, a_scale, w_scale,
+                                           out, workspace, int(m), int(n), int(k), 0,
+                                           as_stream(stream)));
+}
+
+int ci8_channel_mm(const int8_t* a, const uint8_t* w_u8, const float* a_scale,
+                   const void* w_scale, void* out, int64_t m, int64_t n, int64_t k,
+                   void* stream) {
+  if (!(m > 0 && n > 0 && k > 0 && k % 32 == 0 && k <= 65536))
+    return fail(CI8_ERR_GEOMETRY, "Invalid matrix geometry");
+  if (m * k > INT_MAX || n * k > INT_MAX || m * n > INT_MAX)
+    return fail(CI8_ERR_TOO_LARGE, "Matrix too large");
+  if (!aligned(a, 16) || !aligned(w_u8, 16) || !aligned(a_scale, 4) || !aligned(w_scale, 2) ||
+      !aligned(out, 2))
+    return fail(CI8_ERR_ALIGNMENT, "channel_mm requires aligned buffers");
+  return launched(ci8::launch_channel_gemm(a, w_u8, ci8::WeightCode::kBiasedU8, a_scale,
+                                           w_scale, out, nullptr, int(m), int(n), int(k), 0,
+                                           as_stream(stream)));
+}
+
+int ci8_channel_gemv(const void* x, const int8_t* w, const void* scale, void* out, int64_t m,
+                     int64_t n, int64_t k, void* stream) {
+  if (!(m > 0 && m <= 16 && n > 0 && k > 0 && k <= 65536 && k % 16 == 0))
+    return fail(CI8_ERR_GEOMETRY, "Unsupported W8A16 GEMV geometry");
+  if (n * k > INT_MAX) return fail(CI8_ERR_TOO_LARGE, "Weight matrix too large");
+  if (!aligned(w, 16) || !aligned(x, 4) || !aligned(scale, 2) || !aligned(out, 2))
+    return fail(CI8_ERR_ALIGNMENT, "Unaligned vector inputs");
+  return launched(
+      ci8::launch_channel_gemv(x, w, scale, out, int(m), int(n), int(k), as_stream(stream)));
+}
+
+}  // extern "C"

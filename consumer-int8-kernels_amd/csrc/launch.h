@@ -1,0 +1,27 @@
+// Internal host launchers (C++), called by the validated C ABI in abi.cpp. Arguments
+// are assumed valid; each returns the launch status.
+#pragma once
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+namespace ci8 {
+
+hipError_t launch_quantize_rows(const void* x, int8_t* codes, float* scales, int m, int k,
+                                hipStream_t stream);
+// x [m, groups, k] -> codes [groups, m, k], scales [groups, m].
+hipError_t launch_quantize_grouped(const void* x, int8_t* codes, float* scales, int m,
+                                   int groups, int k, hipStream_t stream);
+
+// Weight encodings accepted by the GEMM.
+enum class WeightCode { kSigned, kBiasedU8 };
+
+// out = bf16((float(A W^T) * sa) * sw); optional INT32 copy of the accumulators.
+hipError_t launch_channel_gemm(const int8_t* a, const void* w, WeightCode code,
+                               const float* sa, const void* sw, void* out,
+                               int32_t* workspace, int m, int n, int k, int schedule,
+                               hipStream_t stream);
+
+hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale, void* out,
+                               int m, int n, int k, hipStream_t stream);
+
+}  // namespace ci8

@@ -1,0 +1,166 @@
+// Row quantizers for gfx950: BF16 [rows, k] -> INT8 codes + FP32 per-row scales.
+//
+// Numerics follow csrc/kernels.cu:13-35 and :41-86 of the reference exactly:
+//   amax  = NaN-ignoring max |x| over the row, starting from 0
+//   scale = max(fl(amax / 127), 1e-20f)                       (IEEE division)
+//   code  = clamp(rne(fl(x / scale)), -127, 127)              (IEEE division, RNE)
+// fl(x/scale) never exceeds 127 in magnitude for finite x, so the clamp only matters
+// for non-finite input; rounding uses the 1.5*2^23 add, whose low byte is the
+// two's-complement code and which maps NaN to 0 like the reference's
+// float->int conversion.
+//
+// Layout: every wave owns one row (or a quarter of one, for very wide rows) and keeps
+// the whole row in registers between the max reduction and the store, so HBM sees a
+// single read of x and a single write of the codes, with 16-byte loads and 8-byte
+// stores fully coalesced across the wave.
+#include "ci8_device.h"
+#include "launch.h"
+
+namespace ci8 {
+namespace {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int offset = 32; offset >= 1; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, kWave));
+  return v;
+}
+
+// rne(q) for |q| <= 127.5 as the low byte of fl(q + 1.5*2^23); NaN -> 0.
+__device__ __forceinline__ uint32_t code_byte(float q) {
+  return __float_as_uint(q + 12582912.0f) & 0xFFu;
+}
+
+// Vector path. Requires k % 8 == 0, x 16-byte aligned, codes 8-byte aligned.
+// kWaves waves cooperate on one row when kWaves > 1 (very wide rows).
+// Grouped: output row o reads input row (o % m) * groups + o / m ([m,g,k] -> [g,m,k]).
+template <int kPacks, int kWaves, bool kGrouped>
+__global__ void __launch_bounds__(256) quantize_rows_vec_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ codes, float* __restrict__ scales,
+    int rows, int k, int m, int groups) {
+  constexpr int kRowsPerBlock = 4 / kWaves;
+  __shared__ float partial[4];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int out_row = blockIdx.x * kRowsPerBlock + wave / kWaves;
+  const int part = wave % kWaves;
+  const bool active = out_row < rows;
+  const int64_t in_row = kGrouped ? int64_t(out_row % m) * groups + out_row / m : out_row;
+  const uint16_t* src = x + in_row * k;
+
+  u32x4 packed[kPacks];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPacks; ++i) {
+    const int col = ((i * kWaves + part) * kWave + lane) * 8;
+    packed[i] = u32x4{0, 0, 0, 0};
+    if (active && col < k) packed[i] = *reinterpret_cast<const u32x4*>(src + col);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t word = packed[i][j];
+      amax = fmaxf(amax, fabsf(__uint_as_float(word << 16)));
+      amax = fmaxf(amax, fabsf(__uint_as_float(word & 0xFFFF0000u)));
+    }
+  }
+  amax = wave_max(amax);
+  if constexpr (kWaves > 1) {
+    if (lane == 0) partial[wave] = amax;
+    __syncthreads();
+    amax = partial[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) amax = fmaxf(amax, partial[w]);
+  }
+  if (!active) return;
+  const float scale = fmaxf(amax / 127.f, 1e-20f);
+  if (part == 0 && lane == 0) scales[out_row] = scale;
+  int8_t* dst = codes + int64_t(out_row) * k;
+#pragma unroll
+  for (int i = 0; i < kPacks; ++i) {
+    const int col = ((i * kWaves + part) * kWave + lane) * 8;
+    if (col < k) {
+      uint32_t out[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        uint32_t bytes = 0;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const uint32_t word = packed[i][h * 2 + j];
+          const float lo = __uint_as_float(word << 16) / scale;
+          const float hi = __uint_as_float(word & 0xFFFF0000u) / scale;
+          bytes |= code_byte(lo) << (16 * j);
+          bytes |= code_byte(hi) << (16 * j + 8);
+        }
+        out[h] = bytes;
+      }
+      *reinterpret_cast<u32x2*>(dst + col) = u32x2{out[0], out[1]};
+    }
+  }
+}
+
+// Fallback for any k and any 2-byte alignment: one wave per row, two passes.
+template <bool kGrouped>
+__global__ void __launch_bounds__(256) quantize_rows_scalar_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ codes, float* __restrict__ scales,
+    int rows, int k, int m, int groups) {
+  const int lane = threadIdx.x & 63;
+  const int out_row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (out_row >= rows) return;
+  const int64_t in_row = kGrouped ? int64_t(out_row % m) * groups + out_row / m : out_row;
+  const uint16_t* src = x + in_row * k;
+  float amax = 0.f;
+  for (int col = lane; col < k; col += kWave) amax = fmaxf(amax, fabsf(bf16_to_f32(src[col])));
+  amax = wave_max(amax);
+  const float scale = fmaxf(amax / 127.f, 1e-20f);
+  if (lane == 0) scales[out_row] = scale;
+  int8_t* dst = codes + int64_t(out_row) * k;
+  for (int col = lane; col < k; col += kWave)
+    dst[col] = static_cast<int8_t>(code_byte(bf16_to_f32(src[col]) / scale));
+}
+
+template <bool kGrouped>
+hipError_t dispatch(const void* x, int8_t* codes, float* scales, int rows, int k, int m,
+                    int groups, hipStream_t stream) {
+  const auto* src = static_cast<const uint16_t*>(x);
+  const bool vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
+                   (reinterpret_cast<uintptr_t>(codes) % 8 == 0) && (k % 8 == 0);
+  const int packs = (k + 511) / 512;  // 16-byte packs per lane with one wave per row
+#define CI8_Q1(P)                                                                          \
+  if (packs <= P) {                                                                        \
+    quantize_rows_vec_kernel<P, 1, kGrouped><<<(rows + 3) / 4, 256, 0, stream>>>(          \
+        src, codes, scales, rows, k, m, groups);                                           \
+    return hipGetLastError();                                                              \
+  }
+#define CI8_Q4(P)                                                                          \
+  if (packs <= 4 * P) {                                                                    \
+    quantize_rows_vec_kernel<P, 4, kGrouped><<<rows, 256, 0, stream>>>(                    \
+        src, codes, scales, rows, k, m, groups);                                           \
+    return hipGetLastError();                                                              \
+  }
+  if (vec) {
+    CI8_Q1(1) CI8_Q1(2) CI8_Q1(3) CI8_Q1(4) CI8_Q1(5) CI8_Q1(6) CI8_Q1(7) CI8_Q1(8)
+    CI8_Q1(9) CI8_Q1(10) CI8_Q1(12) CI8_Q1(14) CI8_Q1(16) CI8_Q1(18) CI8_Q1(20)
+    CI8_Q1(24) CI8_Q1(28) CI8_Q1(32) CI8_Q1(36)
+    CI8_Q4(10) CI8_Q4(12) CI8_Q4(16) CI8_Q4(20) CI8_Q4(24) CI8_Q4(32)
+  }
+#undef CI8_Q1
+#undef CI8_Q4
+  quantize_rows_scalar_kernel<kGrouped><<<(rows + 3) / 4, 256, 0, stream>>>(
+      src, codes, scales, rows, k, m, groups);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_quantize_rows(const void* x, int8_t* codes, float* scales, int m, int k,
+                                hipStream_t stream) {
+  return dispatch<false>(x, codes, scales, m, k, m, 1, stream);
+}
+
+hipError_t launch_quantize_grouped(const void* x, int8_t* codes, float* scales, int m,
+                                   int groups, int k, hipStream_t stream) {
+  if (m == 0) return hipSuccess;
+  return dispatch<true>(x, codes, scales, m * groups, k, m, groups, stream);
+}
+
+}  // namespace ci8

@@ -1,0 +1,110 @@
+/* consumer_int8_amd.h -- C ABI of the MI355X (gfx950) INT8 linear-layer hot path.
+ *
+ * Every entry point takes raw device pointers, int64 sizes and a HIP stream passed as
+ * `void*` (a hipStream_t; NULL selects the null stream). Calls are asynchronous and
+ * stream-ordered, allocate nothing, keep no mutable global state and write only the
+ * caller-owned outputs, so they can be captured into a HIP graph.
+ *
+ * Each function validates its arguments before touching the GPU. A rejected call
+ * returns a CI8_ERR_* code without launching anything; the message is available from
+ * ci8_last_error() on the calling thread. A launch failure returns CI8_ERR_LAUNCH.
+ *
+ * Reference interfaces each entry point replaces (AppMana/consumer-int8-kernels):
+ *   ci8_quantize_rows        csrc/kernels.h:48-49 (host launcher), csrc/bindings.cpp:191-209
+ *                            (validation), op schema csrc/bindings.cpp:603
+ *   ci8_quantize_grouped4096 csrc/kernels.h:50-51, csrc/bindings.cpp:210-237, schema :604
+ *   ci8_fused_channel_mm     csrc/kernels.h:27-28, csrc/bindings.cpp:386-427, schema :598
+ *   ci8_cutlass_channel_mm   csrc/kernels.h:63-65, csrc/bindings.cpp:386-424, schema :610
+ *   ci8_channel_mm           csrc/kernels.h:56-58, csrc/bindings.cpp:238-265, schema :605
+ *   ci8_channel_gemv         csrc/kernels.h:54-55, csrc/bindings.cpp:289-310, schema :606
+ */
+#ifndef CONSUMER_INT8_AMD_H
+#define CONSUMER_INT8_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. The message of a failed call carries the same wording as the
+ * reference's RuntimeError for the same condition. */
+enum ci8_status {
+  CI8_OK = 0,
+  CI8_ERR_GEOMETRY = 1,  /* shapes or sizes the op does not accept */
+  CI8_ERR_ALIGNMENT = 2, /* a buffer the kernels read with vector loads is misaligned */
+  CI8_ERR_OVERLAP = 3,   /* outputs overlap inputs or each other */
+  CI8_ERR_SCHEDULE = 4,  /* fused_channel_mm schedule outside 0..6 */
+  CI8_ERR_TOO_LARGE = 5, /* a matrix exceeds INT_MAX elements */
+  CI8_ERR_LAUNCH = 6     /* the HIP runtime reported an error at launch */
+};
+
+/* Message of the last failed call on this thread ("" after a successful call). */
+const char* ci8_last_error(void);
+
+/* Library version string, e.g. "0.1.0". */
+const char* ci8_version(void);
+
+/* quantize_rows: x BF16 [m,k] (row-major, any 2-byte alignment) -> codes INT8 [m,k]
+ * and scales FP32 [m]. Per row: scale = max(amax/127, 1e-20f) with amax the
+ * NaN-ignoring max |x|; code = clamp(rne(x/scale), -127, 127) with IEEE division.
+ * Requires m > 0, k > 0, m*k <= INT_MAX.
+ * Replaces: quantize_rows(const void*, int8_t*, float*, int m, int k, cudaStream_t),
+ *           csrc/kernels.h:48-49; checks of csrc/bindings.cpp:199-203. */
+int ci8_quantize_rows(const void* x, int8_t* codes, float* scales, int64_t m, int64_t k,
+                      void* stream);
+
+/* quantize_grouped4096: x BF16 [m,groups,4096] -> codes INT8 [groups,m,4096] and
+ * scales FP32 [groups,m]; each (row, group) quantized exactly as quantize_rows.
+ * m = 0 is a no-op. Requires groups > 0, x 16-byte, codes 8-byte and scales 4-byte
+ * aligned, and no overlap between the three buffers.
+ * Replaces: quantize_grouped4096(const void*, int8_t*, float*, int m, int groups,
+ *           cudaStream_t), csrc/kernels.h:50-51; checks of csrc/bindings.cpp:216-232. */
+int ci8_quantize_grouped4096(const void* x, int8_t* codes, float* scales, int64_t m,
+                             int64_t groups, void* stream);
+
+/* fused_channel_mm: out BF16 [m,n] = bf16_rn((float(acc) * a_scale[m]) * float(w_scale[n]))
+ * with acc = sum_k a[m,k] * w[n,k] exact in INT32; a INT8 [m,k], w INT8 [n,k] (both
+ * K-contiguous), a_scale FP32 [m], w_scale BF16 [n]. No workspace.
+ * Requires m,n,k > 0, n % 4 == 0, k % 32 == 0, k <= 65536, each matrix <= INT_MAX
+ * elements, schedule in 0..6 (a tiling hint; every schedule gives identical bits).
+ * Replaces: fused_channel_mm(const int8_t*, const int8_t*, const float*, const void*,
+ *           void*, int m, int n, int k, int schedule, cudaStream_t), csrc/kernels.h:27-28;
+ *           checks of csrc/bindings.cpp:402-412. */
+int ci8_fused_channel_mm(const int8_t* a, const int8_t* w, const float* a_scale,
+                         const void* w_scale, void* out, int64_t m, int64_t n, int64_t k,
+                         int64_t schedule, void* stream);
+
+/* cutlass_channel_mm: as fused_channel_mm, and also stores the exact INT32
+ * accumulators in workspace INT32 [m,n].
+ * Replaces: cutlass_channel_mm(..., int32_t* workspace, void* out, int m, int n, int k,
+ *           cudaStream_t), csrc/kernels.h:63-65; checks of csrc/bindings.cpp:402-408. */
+int ci8_cutlass_channel_mm(const int8_t* a, const int8_t* w, const float* a_scale,
+                           const void* w_scale, int32_t* workspace, void* out, int64_t m,
+                           int64_t n, int64_t k, void* stream);
+
+/* channel_mm: as fused_channel_mm with biased UINT8 weights w_u8 [n,k] holding
+ * signed code + 128 (the weight used is w_u8 - 128). Any n > 0.
+ * Requires m,n,k > 0, k % 32 == 0, k <= 65536, a and w <= INT_MAX elements.
+ * Replaces: channel_mm(const int8_t*, const uint8_t*, const float*, const void*, void*,
+ *           int m, int n, int k, cudaStream_t), csrc/kernels.h:56-58;
+ *           checks of csrc/bindings.cpp:252-258. */
+int ci8_channel_mm(const int8_t* a, const uint8_t* w_u8, const float* a_scale,
+                   const void* w_scale, void* out, int64_t m, int64_t n, int64_t k,
+                   void* stream);
+
+/* channel_gemv (W8A16): out BF16 [m,n] = bf16_rn(sum_k float(x[m,k]) * wq[n,k]) with
+ * wq[n,k] = bf16_rn(float(w[n,k]) * float(scale[n])) and FP32 accumulation; x BF16
+ * [m,k], w INT8 [n,k], scale BF16 [n].
+ * Requires 0 < m <= 16 (the reference accepts m <= 8), n > 0, 0 < k <= 65536,
+ * k % 16 == 0, w <= INT_MAX elements, w 16-byte and x 4-byte aligned.
+ * Replaces: channel_gemv(const void*, const int8_t*, const void*, void*, int m, int n,
+ *           int k, cudaStream_t), csrc/kernels.h:54-55; checks of csrc/bindings.cpp:298-305. */
+int ci8_channel_gemv(const void* x, const int8_t* w, const void* scale, void* out,
+                     int64_t m, int64_t n, int64_t k, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CONSUMER_INT8_AMD_H */

@@ -1,0 +1,237 @@
+"""CPU oracle for the INT8 linear-layer hot path -- TEST INFRASTRUCTURE ONLY.
+
+This module restates, in numpy, the arithmetic of AppMana/consumer-int8-kernels for
+quantize_rows, quantize_grouped4096, fused/cutlass_channel_mm, channel_mm, channel_gemv
+and the channel weight encoding. Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import it, and only as the checker (or the timed CPU baseline);
+the product path never calls it and has no CPU fallback.
+
+Every function cites the reference file:line it follows. How each one is pinned
+(known-answer tests, closed forms, exhaustive and brute-force checks) is in
+tests/test_oracle.py; the grouped-and-summed W8A8 closed form (grouped_summed_mm) has
+no reference op and is pinned only by its own definition and brute force.
+
+Conventions: BF16 tensors are carried as uint16 bit patterns, so no library rounding
+is involved anywhere; FP32 arithmetic is numpy float32 (IEEE-754, round to nearest
+even, correctly rounded division).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+F32_TINY = np.float32(np.finfo(np.float32).tiny)
+SCALE_FLOOR = np.float32(1e-20)  # csrc/kernels.cu:27 and :70 (fmaxf(amax / 127.f, 1e-20f))
+
+
+# ---------------------------------------------------------------- BF16 <-> FP32
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    """Exact widening of BF16 bit patterns (uint16) to float32."""
+    bits = np.asarray(bits, dtype=np.uint16)
+    return (bits.astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def f32_to_bf16(values: np.ndarray) -> np.ndarray:
+    """float32 -> BF16 bits with IEEE round-to-nearest-even; NaN stays NaN (quieted).
+
+    This is __float2bfloat16 / cutlass round_to_nearest as used at csrc/gemv.cu:25,
+    csrc/kernels.cu:120 and csrc/fused_mm.cu:33-37.
+    """
+    values = np.asarray(values, dtype=np.float32)
+    bits = values.view(np.uint32).astype(np.uint64)
+    rounded = (bits + np.uint64(0x7FFF) + ((bits >> np.uint64(16)) & np.uint64(1))) >> np.uint64(16)
+    nan = np.isnan(values)
+    quiet = ((bits >> np.uint64(16)) | np.uint64(0x0040))
+    return np.where(nan, quiet, rounded).astype(np.uint16)
+
+
+def f64_to_bf16(values: np.ndarray) -> np.ndarray:
+    """float64 -> BF16 bits by way of float32 (both steps round to nearest even).
+
+    Mirrors the reference test oracle, which rounds an FP64 result with .bfloat16()
+    after it is cast (tests/test_gemv.py:27-29 via torch's double->bfloat16 path).
+    """
+    return f32_to_bf16(np.asarray(values, dtype=np.float64).astype(np.float32))
+
+
+# ---------------------------------------------------------------- quantizers
+
+def quantize_rows(x_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """BF16 [M, K] bits -> (INT8 codes [M, K], FP32 scales [M]).
+
+    csrc/kernels.cu:13-35 (scalar) and :41-86 (vector), which agree:
+      amax  = fmaxf-reduction of |x| starting at 0 (NaN ignored)        :16-26, :56-69
+      scale = fmaxf(amax / 127.f, 1e-20f)                                :27, :70
+      code  = clamp(__float2int_rn(x / scale), -127, 127)               :33, :81-82
+    __float2int_rn maps NaN to 0; fl(x/scale) never exceeds 127.0000077 for finite x.
+    """
+    x = bf16_to_f32(x_bits)
+    amax = np.fmax.reduce(np.abs(x), axis=-1, initial=np.float32(0)).astype(np.float32)
+    scale = np.fmax(amax / np.float32(127.0), SCALE_FLOOR).astype(np.float32)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        q = (x / scale[..., None]).astype(np.float32)
+    q = np.rint(q)
+    q = np.where(np.isnan(q), np.float32(0), q)
+    q = np.clip(q, -127, 127).astype(np.int8)
+    return q, scale
+
+
+def quantize_grouped4096(x_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """BF16 [M, G, 4096] -> (codes [G, M, 4096], scales [G, M]).
+
+    csrc/kernels.cu:46-48 (output row b reads input row (b % M)*G + b / M) and
+    :293-298 (M = 0 is a no-op); equal to quantize_rows on x[:, g]
+    (tests/test_cuda_ops.py:31-38).
+    """
+    m, g, k = x_bits.shape
+    assert k == 4096
+    codes, scales = quantize_rows(np.ascontiguousarray(x_bits.transpose(1, 0, 2)).reshape(g * m, k))
+    return codes.reshape(g, m, k), scales.reshape(g, m)
+
+
+# ---------------------------------------------------------------- W8A8 GEMMs
+
+def int_matmul(a: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """Exact INT32 accumulators acc[m, n] = sum_k a[m, k] * w[n, k].
+
+    The reference oracle is the CPU integer product a.int() @ w.int().T
+    (tests/test_cuda_ops.py:596, :488). Here the same integers are summed in float64
+    through BLAS: every product is at most 128*128 = 2^14 in magnitude and every
+    partial sum at most K * 2^14 <= 2^30 < 2^53, so each float64 operation is exact
+    whatever the summation order, and the result is the exact integer.
+    """
+    a = np.asarray(a)
+    w = np.asarray(w)
+    assert a.shape[1] == w.shape[1] and a.shape[1] <= 65536
+    acc = a.astype(np.float64) @ w.astype(np.float64).T
+    return acc.astype(np.int64).astype(np.int32)
+
+
+def channel_epilogue(acc: np.ndarray, sa: np.ndarray, sw_bits: np.ndarray) -> np.ndarray:
+    """bf16_rn( fl( fl(float_rn(acc) * sa[m]) * float(sw[n]) ) ).
+
+    csrc/fused_mm.cu:24-38 (EVT: accumulator x row scale in FP32, then x channel scale,
+    then BF16 round to nearest), csrc/cutlass_mm.cu:35 and csrc/kernels.cu:120 (same
+    left-to-right order); the row scale is applied first (README.md:111-113; the
+    opposite order is a known mismatch, benchmarks/consumer_arch.py:124-129).
+    """
+    accf = np.asarray(acc, dtype=np.int32).astype(np.float32)  # int32 -> float32, RNE
+    sa = np.asarray(sa, dtype=np.float32)
+    swf = bf16_to_f32(sw_bits)
+    with np.errstate(over="ignore", invalid="ignore"):
+        first = (accf * sa[:, None]).astype(np.float32)
+        second = (first * swf[None, :]).astype(np.float32)
+    return f32_to_bf16(second)
+
+
+def fused_channel_mm(a, w, sa, sw_bits) -> np.ndarray:
+    """fused_channel_mm (csrc/fused_mm.cu:17-93): BF16 bits [M, N]."""
+    return channel_epilogue(int_matmul(a, w), sa, sw_bits)
+
+
+def cutlass_channel_mm(a, w, sa, sw_bits) -> tuple[np.ndarray, np.ndarray]:
+    """cutlass_channel_mm (csrc/cutlass_mm.cu:10-50): (INT32 workspace, BF16 bits)."""
+    acc = int_matmul(a, w)
+    return acc, channel_epilogue(acc, sa, sw_bits)
+
+
+def debias(w_u8: np.ndarray) -> np.ndarray:
+    """Biased UINT8 -> signed code: u ^ 0x80 == u - 128 (csrc/kernels.cu:107)."""
+    return (np.asarray(w_u8, dtype=np.uint8) ^ np.uint8(0x80)).view(np.int8)
+
+
+def channel_mm(a, w_u8, sa, sw_bits) -> np.ndarray:
+    """channel_mm (csrc/kernels.cu:88-122): biased UINT8 weights, same epilogue."""
+    return channel_epilogue(int_matmul(a, debias(w_u8)), sa, sw_bits)
+
+
+def grouped_summed_mm(codes, scales, w, sw_bits) -> np.ndarray:
+    """Grouped W8A8 with the per-group partials scaled and summed (no reference op).
+
+    codes INT8 [G, M, Kg], scales FP32 [G, M], w INT8 [G, N, Kg], sw BF16 [N]:
+      out[m, n] = bf16_rn( sum_g fl( fl(float_rn(acc_g[m, n]) * sa[g, m]) * float(sw[n]) ) )
+    summed over ascending g with FP32 additions. Per-group terms follow the
+    fused_channel_mm epilogue; the FP32 sum of scaled INT32 partials follows
+    benchmarks/cuda/q8_block_int8.cu:54-55. Parity of this closed form is unpinned by
+    the reference (it has no such op).
+    """
+    g_count = codes.shape[0]
+    swf = bf16_to_f32(sw_bits)
+    total = None
+    for g in range(g_count):
+        acc = int_matmul(codes[g], w[g]).astype(np.float32)
+        with np.errstate(over="ignore", invalid="ignore"):
+            term = ((acc * np.asarray(scales[g], np.float32)[:, None]).astype(np.float32)
+                    * swf[None, :]).astype(np.float32)
+        total = term if total is None else (total + term).astype(np.float32)
+    return f32_to_bf16(total)
+
+
+# ---------------------------------------------------------------- W8A16 GEMV
+
+def dequantize_bf16(w: np.ndarray, scale_bits: np.ndarray) -> np.ndarray:
+    """wq[n, k] = bf16_rn(float(code) * float(scale[n])) as bits (csrc/gemv.cu:25)."""
+    prod = (np.asarray(w, dtype=np.int8).astype(np.float32)
+            * bf16_to_f32(scale_bits)[:, None]).astype(np.float32)
+    return f32_to_bf16(prod)
+
+
+def channel_gemv(x_bits, w, scale_bits) -> tuple[np.ndarray, np.ndarray]:
+    """channel_gemv reference: (BF16 bits [M, N], exact-ish float64 values [M, N]).
+
+    FP64 dot product of the BF16 activations with the BF16-dequantized weights,
+    rounded to BF16 -- the reference test oracle (tests/test_gemv.py:26-29) for the
+    kernel at csrc/gemv.cu:8-59.
+    """
+    xf = bf16_to_f32(x_bits).astype(np.float64)
+    wq = bf16_to_f32(dequantize_bf16(w, scale_bits)).astype(np.float64)
+    exact = xf @ wq.T
+    return f64_to_bf16(exact), exact
+
+
+def gemv_abs_bound(x_bits, w, scale_bits) -> np.ndarray:
+    """Worst-case FP32 summation error bound K * 2^-24 * sum_k |x * wq| per output."""
+    xf = np.abs(bf16_to_f32(x_bits).astype(np.float64))
+    wq = np.abs(bf16_to_f32(dequantize_bf16(w, scale_bits)).astype(np.float64))
+    k = xf.shape[1]
+    return k * 2.0**-24 * (xf @ wq.T)
+
+
+def bf16_ulp(values: np.ndarray) -> np.ndarray:
+    """Spacing of BF16 numbers at |values| (8 significand bits)."""
+    v = np.abs(np.asarray(values, dtype=np.float64))
+    exp = np.floor(np.log2(np.where(v > 0, v, 2.0**-126)))
+    exp = np.maximum(exp, -126)
+    return 2.0 ** (exp - 7)
+
+
+# ---------------------------------------------------------------- weight encoding
+
+def quantize_channel(weight: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """[N, K] float -> (biased UINT8 codes [N, K], BF16 scale bits [N]).
+
+    src/consumer_int8/quantization.py:22-32: scale = max(amax_row, FP32 tiny) / 127 in
+    FP32; codes = clamp(rne(w / scale), -128, 127) + 128; the stored scale is the BF16
+    rounding of the FP32 scale, taken after the codes. Rejects non-finite weights and
+    scales that round to zero or infinity in BF16 (:16-17, :30-31).
+    """
+    value = np.asarray(weight, dtype=np.float32)
+    if value.ndim != 2 or value.size == 0:
+        raise ValueError("Expected a nonempty floating-point weight matrix")
+    if not np.isfinite(value).all():
+        raise ValueError("Weight contains non-finite values")
+    scale = np.maximum(np.abs(value).max(axis=1), F32_TINY).astype(np.float32)
+    scale = (scale / np.float32(127.0)).astype(np.float32)
+    codes = np.clip(np.rint((value / scale[:, None]).astype(np.float32)), -128, 127)
+    stored = f32_to_bf16(scale)
+    stored_f = bf16_to_f32(stored)
+    if not np.isfinite(stored_f).all() or (stored_f == 0).any():
+        raise ValueError("Channel scales are not representable as nonzero BF16")
+    return (codes.astype(np.int16) + 128).astype(np.uint8), stored
+
+
+def dequantize_channel(codes_u8: np.ndarray, scale_bits: np.ndarray) -> np.ndarray:
+    """(codes - 128) * scale in FP32 (src/consumer_int8/quantization.py:46-47)."""
+    return ((np.asarray(codes_u8).astype(np.float32) - np.float32(128))
+            * bf16_to_f32(scale_bits)[:, None]).astype(np.float32)

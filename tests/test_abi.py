@@ -1,0 +1,160 @@
+"""CPU checks of the drop-in boundary: the C ABI library and the torch op surface.
+
+No kernel is launched here. Every rejection is exercised through the C ABI with fake
+(never dereferenced) pointers, because validation runs before any HIP call.
+"""
+
+import ctypes
+import re
+
+import pytest
+
+from tests.conftest import HEADER_PATH, LIB_PATH
+
+
+def declared_functions():
+    text = HEADER_PATH.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(ci8_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_expected_entry_points():
+    assert declared_functions() == sorted([
+        "ci8_last_error", "ci8_version", "ci8_quantize_rows", "ci8_quantize_grouped4096",
+        "ci8_fused_channel_mm", "ci8_cutlass_channel_mm", "ci8_channel_mm",
+        "ci8_channel_gemv",
+    ])
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_ctypes_binding_covers_header(lib):
+    from consumer_int8 import _abi
+
+    assert sorted(_abi.SIGNATURES) == declared_functions()
+    assert lib.ci8_version().decode().count(".") == 2
+
+
+FAKE = 0x10000  # 64 KiB-aligned fake device address, never dereferenced
+
+
+def expect(lib, status, code, text):
+    from consumer_int8 import _abi
+
+    assert status == code, (status, _abi.last_error())
+    assert text in _abi.last_error()
+
+
+def test_quantize_rows_rejections(lib):
+    from consumer_int8 import _abi as A
+
+    expect(lib, lib.ci8_quantize_rows(FAKE, FAKE, FAKE, 0, 8, None), A.CI8_ERR_GEOMETRY,
+           "Expected a nonempty BF16 matrix")
+    expect(lib, lib.ci8_quantize_rows(FAKE, FAKE, FAKE, 4, 0, None), A.CI8_ERR_GEOMETRY,
+           "nonempty")
+    expect(lib, lib.ci8_quantize_rows(FAKE, FAKE, FAKE, 1 << 16, 1 << 16, None),
+           A.CI8_ERR_TOO_LARGE, "Matrix too large")
+    expect(lib, lib.ci8_quantize_rows(FAKE + 1, FAKE, FAKE, 4, 8, None), A.CI8_ERR_ALIGNMENT,
+           "aligned")
+
+
+def test_grouped_rejections(lib):
+    from consumer_int8 import _abi as A
+
+    msg = "Expected BF16 input[M,G,4096], INT8 codes[G,M,4096], FP32 scales[G,M]"
+    expect(lib, lib.ci8_quantize_grouped4096(FAKE, FAKE, FAKE, 3, 0, None), A.CI8_ERR_GEOMETRY, msg)
+    expect(lib, lib.ci8_quantize_grouped4096(FAKE, FAKE, FAKE, -1, 4, None), A.CI8_ERR_GEOMETRY, msg)
+    expect(lib, lib.ci8_quantize_grouped4096(FAKE + 2, 1 << 30, 1 << 31, 3, 4, None),
+           A.CI8_ERR_ALIGNMENT, "Grouped quantization requires aligned buffers")
+    # codes start inside x (3*4*4096*2 bytes long)
+    expect(lib, lib.ci8_quantize_grouped4096(FAKE, FAKE + 4096, 1 << 31, 3, 4, None),
+           A.CI8_ERR_OVERLAP, "must not overlap")
+    expect(lib, lib.ci8_quantize_grouped4096(1 << 20, 1 << 24, (1 << 24) + 8, 3, 4, None),
+           A.CI8_ERR_OVERLAP, "must not overlap")
+
+
+@pytest.mark.parametrize("m,n,k", [(0, 4, 32), (4, 0, 32), (4, 4, 0), (4, 4, 33), (4, 6, 32),
+                                   (4, 4, 65568)])
+def test_fused_and_cutlass_geometry_rejections(lib, m, n, k):
+    from consumer_int8 import _abi as A
+
+    expect(lib, lib.ci8_fused_channel_mm(FAKE, FAKE, FAKE, FAKE, FAKE, m, n, k, 0, None),
+           A.CI8_ERR_GEOMETRY, "Invalid CUTLASS geometry")
+    expect(lib, lib.ci8_cutlass_channel_mm(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, m, n, k, None),
+           A.CI8_ERR_GEOMETRY, "Invalid CUTLASS geometry")
+
+
+def test_fused_schedule_alignment_and_size_rejections(lib):
+    from consumer_int8 import _abi as A
+
+    for schedule in (-1, 7):
+        expect(lib, lib.ci8_fused_channel_mm(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 4, 32, schedule,
+                                             None), A.CI8_ERR_SCHEDULE,
+               "Invalid fused GEMM schedule")
+    expect(lib, lib.ci8_fused_channel_mm(FAKE + 8, FAKE, FAKE, FAKE, FAKE, 4, 4, 32, 0, None),
+           A.CI8_ERR_ALIGNMENT, "aligned")
+    expect(lib, lib.ci8_fused_channel_mm(FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 16, 4, 1 << 16, 0,
+                                         None), A.CI8_ERR_TOO_LARGE, "Matrix too large")
+
+
+def test_channel_mm_and_gemv_rejections(lib):
+    from consumer_int8 import _abi as A
+
+    expect(lib, lib.ci8_channel_mm(FAKE, FAKE, FAKE, FAKE, FAKE, 1, 4, 33, None),
+           A.CI8_ERR_GEOMETRY, "Invalid matrix geometry")
+    for m, n, k in [(0, 8, 64), (17, 8, 64), (1, 0, 64), (1, 8, 40), (1, 8, 65552)]:
+        expect(lib, lib.ci8_channel_gemv(FAKE, FAKE, FAKE, FAKE, m, n, k, None),
+               A.CI8_ERR_GEOMETRY, "Unsupported W8A16 GEMV geometry")
+    expect(lib, lib.ci8_channel_gemv(FAKE, FAKE + 4, FAKE, FAKE, 1, 8, 64, None),
+           A.CI8_ERR_ALIGNMENT, "Unaligned vector inputs")
+    expect(lib, lib.ci8_channel_gemv(FAKE + 2, FAKE, FAKE, FAKE, 1, 8, 64, None),
+           A.CI8_ERR_ALIGNMENT, "Unaligned vector inputs")
+
+
+def test_torch_surface_matches_reference_schemas():
+    import torch
+
+    from consumer_int8 import ops
+
+    expected = {
+        "fused_channel_mm": "(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) out, int schedule=0) -> ()",
+        "quantize_rows": "(Tensor input, Tensor(a!) codes, Tensor(b!) scales) -> ()",
+        "quantize_grouped4096": "(Tensor input, Tensor(a!) codes, Tensor(b!) scales) -> ()",
+        "channel_mm": "(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) out) -> ()",
+        "channel_gemv": "(Tensor x, Tensor w, Tensor scale, Tensor(a!) out) -> ()",
+        "cutlass_channel_mm": "(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) workspace, Tensor(b!) out) -> ()",
+    }
+    for name, schema in expected.items():
+        handle = getattr(ops, name)
+        assert handle is getattr(torch.ops.consumer_int8, name)
+        assert str(handle.default._schema) == f"consumer_int8::{name}{schema}"
+
+
+def test_no_cpu_fallback():
+    """The product path has no CPU implementation: CPU tensors are refused."""
+    import torch
+
+    from consumer_int8 import ops
+
+    x = torch.zeros(2, 8, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        ops.quantize_rows(x, torch.empty(2, 8, dtype=torch.int8), torch.empty(2))
+
+
+def test_fake_tensor_registration():
+    """register_fake impls exist (torch.compile / meta tracing of the in-place ops)."""
+    import torch
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from consumer_int8 import ops
+
+    with FakeTensorMode():
+        a = torch.empty(4, 64, dtype=torch.int8)
+        w = torch.empty(8, 64, dtype=torch.int8)
+        sa = torch.empty(4)
+        sw = torch.empty(8, dtype=torch.bfloat16)
+        out = torch.empty(4, 8, dtype=torch.bfloat16)
+        assert ops.fused_channel_mm(a, w, sa, sw, out, 0) is None

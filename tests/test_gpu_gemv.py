@@ -1,0 +1,89 @@
+"""GPU parity of channel_gemv (W8A16) against the FP64 oracle.
+
+Tolerance, as the reference (tests/test_gemv.py:10-33): atol 0.004, rtol 0.008 and
+relative L2 < 0.003 against the FP64 dot of the BF16-dequantized weights; in addition
+every output must lie within 1 BF16 ulp of the exact value plus the worst-case FP32
+summation error K * 2^-24 * sum|x * wq| (the bound of an FP32-accumulated reference).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import bf16_bits, host, randn_bf16, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def check_gemv(out_bits, x_bits, w, s_bits):
+    ref_bits, exact = O.channel_gemv(x_bits, w, s_bits)
+    actual = O.bf16_to_f32(out_bits).astype(np.float64)
+    reference = O.bf16_to_f32(ref_bits).astype(np.float64)
+    np.testing.assert_allclose(actual, reference, atol=0.004, rtol=0.008)
+    norm = np.linalg.norm(reference)
+    if norm > 0:
+        assert np.linalg.norm(actual - reference) / norm < 0.003
+    bound = O.bf16_ulp(exact) + O.gemv_abs_bound(x_bits, w, s_bits)
+    assert np.all(np.abs(actual - exact) <= bound)
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 16])
+@pytest.mark.parametrize("n,k", [(37, 528), (512, 5120)])
+def test_w8a16_small_batch_matches_bf16_dequantized_linear(ops, m, n, k):
+    rng = np.random.default_rng(134)
+    x_bits = randn_bf16(rng, (m, k))
+    w = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    s_bits = O.f32_to_bf16((rng.random(n) * 0.002).astype(np.float32))
+    x = to_dev(x_bits)
+    out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    ops.channel_gemv(x, to_dev(w), to_dev(s_bits), out)
+    graph = torch.cuda.CUDAGraph()
+    wt, st = to_dev(w), to_dev(s_bits)
+    with torch.cuda.graph(graph):
+        ops.channel_gemv(x, wt, st, out)
+    x.mul_(0.75)
+    graph.replay()
+    torch.cuda.synchronize()
+    check_gemv(bf16_bits(out), bf16_bits(x), w, s_bits)
+
+
+@pytest.mark.parametrize("m", [1, 4, 8, 16])
+def test_decode_shape_full_size(ops, m):
+    """Config 2: K = 5120, N = 17408, scales uniform in [1e-3, 1e-2]."""
+    k, n = 5120, 17408
+    rng = np.random.default_rng(2 + m)
+    x_bits = randn_bf16(rng, (m, k))
+    w = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    s_bits = O.f32_to_bf16(rng.uniform(1e-3, 1e-2, n).astype(np.float32))
+    out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    ops.channel_gemv(to_dev(x_bits), to_dev(w), to_dev(s_bits), out)
+    torch.cuda.synchronize()
+    check_gemv(bf16_bits(out), x_bits, w, s_bits)
+
+
+@pytest.mark.parametrize("m,n,k", [(3, 100, 16), (5, 64, 48), (16, 7, 1040), (2, 33, 65536)])
+def test_gemv_tails_and_unaligned_activations(ops, m, n, k):
+    rng = np.random.default_rng(m * n + k)
+    x_bits = randn_bf16(rng, (m, k))
+    w = rng.integers(-128, 128, (n, k)).astype(np.int8)
+    s_bits = O.f32_to_bf16((rng.random(n) * 0.01).astype(np.float32))
+    # x starts 4 bytes past a 16-byte boundary (the reference only asks for 4).
+    storage = to_dev(np.concatenate([np.zeros(2, np.uint16), x_bits.ravel()]))
+    x = storage[2:].view(m, k)
+    out = torch.full((m, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+    ops.channel_gemv(x, to_dev(w), to_dev(s_bits), out)
+    torch.cuda.synchronize()
+    check_gemv(bf16_bits(out), x_bits, w, s_bits)
+
+
+def test_gemv_rejects_unsupported_geometry(ops):
+    x = torch.zeros(17, 64, device="cuda", dtype=torch.bfloat16)
+    w = torch.zeros(8, 64, device="cuda", dtype=torch.int8)
+    s = torch.ones(8, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="Unsupported W8A16 GEMV geometry"):
+        ops.channel_gemv(x, w, s, torch.empty(17, 8, device="cuda", dtype=torch.bfloat16))
+    x = torch.zeros(1, 40, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="geometry"):
+        ops.channel_gemv(x, torch.zeros(8, 40, device="cuda", dtype=torch.int8), s,
+                         torch.empty(1, 8, device="cuda", dtype=torch.bfloat16))
