@@ -53,9 +53,16 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"command failed ({result.returncode}): {' '.join(cmd)}\n{stderr}")
 
 
+# Per-file extra flags. The GEMM's machine scheduler: the default strategy lets the
+# register allocator rotate the 224 MFMA accumulators between AGPRs and VGPRs in the
+# software-pipelined loop (copies around every MFMA); iterative-minreg keeps every
+# accumulator in place.
+FILE_FLAGS = {"gemm.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-minreg"]}
+
+
 def _compile(src: Path, obj: Path) -> Path:
     if src.suffix == ".hip":
-        _run([HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)])
+        _run([HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)])
     else:
         _run([HIPCC, "-O2", "-std=c++17", "-fPIC", "-Wall", f"-I{INCLUDE}", f"-I{CSRC}",
               "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}", "-x", "c++", "-c", str(src), "-o", str(obj)])

@@ -43,7 +43,6 @@ struct TileConfig {
   static constexpr int TN = BN / WN / 32;  // 32x32 MFMA tiles per wave along n
   static constexpr int TM = BM / WM / 32;  // ... along m
   static constexpr int kChunksPerRow = BK / 16;
-  static constexpr int kRowsPer256 = 256 / BK;
   static constexpr int kXBytes = BN * BK;  // one stage of the W tile
   static constexpr int kYBytes = BM * BK;  // one stage of the A tile
   static constexpr int kStageBytes = kXBytes + kYBytes;
@@ -59,10 +58,20 @@ struct TileConfig {
   static_assert(kLdsBytes <= 160 * 1024, "LDS");
 };
 
-// Chunk slot of logical 16-byte chunk c in LDS row r.
+// 16-byte LDS load (ds_read_b128).
+__device__ __forceinline__ i32x4 ld(const char __attribute__((address_space(3)))* p) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) i32x4*>(p);
+}
+
+// Chunk slot of logical 16-byte chunk c in LDS row r. A fragment load has 16
+// consecutive lanes reading 16 consecutive rows at the same logical chunk; the XOR
+// below puts any 8 consecutive rows on distinct 16-byte bank groups of a 128-byte
+// window. Measured on gfx950, this makes ds_read_b128 fragment loads as fast as a
+// linear 1 KiB read, while leaving them unswizzled or using a 256-byte-window variant
+// costs about 12%.
 template <class C>
 __device__ __forceinline__ int swizzle(int row, int chunk) {
-  return chunk ^ ((row / C::kRowsPer256) % C::kChunksPerRow);
+  return chunk ^ ((row / (128 / C::BK)) % C::kChunksPerRow);
 }
 
 // Issue this wave's DMA copies of one K-slice of an operand tile (rows x BK) into LDS.
@@ -96,7 +105,7 @@ __global__ void __launch_bounds__(C::kThreads) channel_gemm_kernel(
   auto* lds = (char __attribute__((address_space(3)))*)(lds_raw);
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int wave_n = wave / C::WM;
   const int wave_m = wave % C::WM;
 
@@ -249,10 +258,357 @@ hipError_t run(const int8_t* a, const void* w, const float* sa, const void* sw, 
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------
+// Pipelined large-tile kernel (v_mfma_i32_16x16x64_i8), K staged 128 bytes at a time.
+//
+// Tile 256(m) x 224(n) per workgroup; four waves (one per SIMD) each own 128 x 112 as
+// 8 x 7 16x16 INT32 accumulators (224 AGPRs). 256 x 224 suits wave quantization on 256
+// CUs: N = 17408 gives 78 n-tiles and M = 4096 gives 16, 1248 tiles = 4.875 rounds
+// (97.5% busy), where 256 x 256 gives 1088 tiles = 4.25 rounds (85%).
+//
+// Feeding: the L2 -> CU path on gfx950 delivers far more when each row segment is a
+// full 128-byte line (measured about 14 TB/s aggregate for 64-byte segments through
+// buffer_load ... lds, 22 TB/s for 128-byte ones), and a 256 x 224 tile at the MFMA
+// rate needs about 17 TB/s. So a stage holds 128 bytes of K per row (60 KB for both
+// operands) and two stages fit in LDS. A stage is two K-steps of one 16x16x64 MFMA
+// each (56 MFMAs per wave per step). For stage t:
+//   step A (K-step 2t):   MFMAs from registers; read the fragments of K-step 2t+1
+//                         from slot t%2;
+//   barrier:              own copies of stage t+1 landed and own reads of slot t%2
+//                         returned (both checked before the barrier), so after it
+//                         stage t+1 is visible and slot t%2 is free;
+//   step B (K-step 2t+1): issue the copies of stage t+2 into slot t%2, MFMAs from
+//                         registers, read the fragments of K-step 2t+2 (stage t+1).
+// Stage t+2's copies therefore have two K-steps (about 1800 MFMA cycles) to land.
+// W fragments are double-buffered in registers; A fragments 0..5 are reloaded in place
+// after their last MFMA, and A fragments 6..7 alternate with a spare pair loaded early,
+// so the last LDS read of step A is issued two MFMA groups before the barrier.
+template <int BM_, int BN_, int WM_, int WN_, int GROUP_M_>
+struct K128Config {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, GROUP_M = GROUP_M_;
+  static constexpr int BK = 128;  // K bytes per stage (two 64-deep MFMA steps)
+  static constexpr int kWaves = WM * WN;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int TM = BM / WM / 16;  // 16-row m blocks per wave
+  static constexpr int TN = BN / WN / 16;  // 16-row n blocks per wave
+  static constexpr int kSpare = 2;         // A fragments with a spare register pair
+  static constexpr int kChunksPerRow = BK / 16;
+  static constexpr int kXBytes = BN * BK;
+  static constexpr int kYBytes = BM * BK;
+  static constexpr int kStageBytes = kXBytes + kYBytes;
+  static constexpr int kXBlocks = kXBytes / 1024;
+  static constexpr int kBlocks = kStageBytes / 1024;
+  static constexpr int kLoads = (kBlocks + kWaves - 1) / kWaves;  // DMA per wave per stage
+  static constexpr int kJunkOffset = 2 * kStageBytes;  // target of padding DMA, if any
+  static constexpr int kLdsBytes = kJunkOffset + (kLoads * kWaves > kBlocks ? 1024 : 0);
+  static_assert(kXBytes % 1024 == 0 && kYBytes % 1024 == 0, "whole 1 KiB blocks");
+  static_assert(TM * 16 * WM == BM && TN * 16 * WN == BN, "wave tiling");
+  static_assert(TM > kSpare, "spare A fragments");
+  static_assert(kLdsBytes <= 160 * 1024, "LDS");
+};
+
+// Wrappers for the target builtins used by the pipelined kernel. Its helper lambdas
+// call these rather than the builtins themselves: a builtin written directly inside a
+// lambda makes the host compilation pass drop the kernel's launch stub.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, lds_void* dst, uint32_t voffset,
+                                      int soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, voffset, soffset, 0, 0);
+}
+template <int kImm>
+__device__ __forceinline__ void waitcnt() {
+  __builtin_amdgcn_s_waitcnt(kImm);
+}
+__device__ __forceinline__ void workgroup_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ i32x4 mfma16(i32x4 a, i32x4 b, i32x4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+template <int kMask, int kSize>
+__device__ __forceinline__ void sched_group() {
+  __builtin_amdgcn_sched_group_barrier(kMask, kSize, 0);
+}
+
+// Scheduling-group barriers that place the in-place reload of A fragment J (J < kLast)
+// after the last MFMA reading it, MFMA (J+1)*TN - 1; P MFMAs are already placed.
+template <int J, int kLast, int TM, int TN, int P>
+struct AReloads {
+  static __device__ __forceinline__ void run() {
+    if constexpr (J < kLast) {
+      constexpr int end = (J + 1) * TN;
+      if constexpr (end > P) sched_group<0x008, end - P>();
+      sched_group<0x100, 1>();
+      AReloads<J + 1, kLast, TM, TN, (end > P ? end : P)>::run();
+    } else if constexpr (TM * TN > P) {
+      sched_group<0x008, TM * TN - P>();
+    }
+  }
+};
+
+template <class C, WeightCode kCode, bool kWorkspace, bool kExactK>
+__global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_k128_kernel(
+    const int8_t* __restrict__ a, const void* __restrict__ w, const float* __restrict__ sa,
+    const uint16_t* __restrict__ sw, uint16_t* __restrict__ out, int32_t* __restrict__ ws,
+    int m, int n, int k, bool vec_n) {
+  extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
+  auto* lds = (char __attribute__((address_space(3)))*)(lds_raw);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+  const int wave_m = wave % C::WM;
+  const int wave_n = wave / C::WM;
+
+  const int tiles_n = (n + C::BN - 1) / C::BN;
+  const int tiles_m = (m + C::BM - 1) / C::BM;
+  const int blocks = tiles_n * tiles_m;
+  int logical = blockIdx.x;
+  {
+    const int per = blocks / kXcds, extra = blocks % kXcds;
+    const int xcd = logical % kXcds, idx = logical / kXcds;
+    logical = (xcd < extra ? xcd * (per + 1) : extra * (per + 1) + (xcd - extra) * per) + idx;
+  }
+  const int group_span = C::GROUP_M * tiles_n;
+  const int first_m = (logical / group_span) * C::GROUP_M;
+  const int group_rows = min(tiles_m - first_m, C::GROUP_M);
+  const int tile_m = first_m + (logical % group_span) % group_rows;
+  const int tile_n = (logical % group_span) / group_rows;
+  const int n0 = tile_n * C::BN, m0 = tile_m * C::BM;
+
+  const auto w_rsrc = make_rsrc(w, uint32_t(n) * uint32_t(k));
+  const auto a_rsrc = make_rsrc(a, uint32_t(m) * uint32_t(k));
+
+  // Per-lane DMA sources for this wave's kLoads 1 KiB blocks of a stage: blocks
+  // [0, kXBlocks) are W rows, then A rows, then padding (out-of-range source into a
+  // scratch KiB). The stage's K offset goes in the scalar soffset.
+  uint32_t dma_base[C::kLoads];
+  int dma_col[C::kLoads];
+#pragma unroll
+  for (int i = 0; i < C::kLoads; ++i) {
+    const int block = i * C::kWaves + wave;
+    const bool is_w = block < C::kXBlocks;
+    const int local = is_w ? block : block - C::kXBlocks;
+    const int q = local * 64 + lane;
+    const int row = q / C::kChunksPerRow;
+    const int chunk = swizzle<C>(row, q % C::kChunksPerRow);  // the swizzle is an involution
+    const int grow = (is_w ? n0 : m0) + row;
+    const bool valid = block < C::kBlocks && grow < (is_w ? n : m);
+    dma_col[i] = chunk * 16;
+    dma_base[i] = valid ? uint32_t(grow) * uint32_t(k) + uint32_t(chunk * 16) : kOutOfRange;
+  }
+#define CI8_DMA_RSRC(i) ((i) * C::kWaves + wave < C::kXBlocks ? w_rsrc : a_rsrc)
+  auto dma_dst = [&] __device__(int i, int slot) __attribute__((always_inline)) {
+    const int block = i * C::kWaves + wave;
+    return reinterpret_cast<lds_void*>(
+        lds + (block < C::kBlocks ? slot * C::kStageBytes + block * 1024 : C::kJunkOffset));
+  };
+  const int ns = (k + C::BK - 1) / C::BK;  // stages
+  // Copies of stage t into slot t % 2. Stages past the end re-read stage 0 into a slot
+  // nobody reads again (keeps the steady loop branch-free).
+  auto issue = [&] __device__(int t) __attribute__((always_inline)) {
+    const int slot = t & 1;
+    const int st = t < ns ? t : 0;
+    if constexpr (kExactK) {
+#pragma unroll
+      for (int i = 0; i < C::kLoads; ++i)
+        dma16(CI8_DMA_RSRC(i), dma_dst(i, slot), dma_base[i], st * C::BK);
+    } else {
+      const int k0 = st * C::BK;
+#pragma unroll
+      for (int i = 0; i < C::kLoads; ++i) {
+        const bool live = dma_base[i] != kOutOfRange && k0 + dma_col[i] < k;
+        dma16(CI8_DMA_RSRC(i), dma_dst(i, slot), live ? dma_base[i] + uint32_t(k0) : kOutOfRange,
+              0);
+      }
+    }
+  };
+
+  // Fragment addresses. A lane reads row (lane % 16) of each 16-row block at logical
+  // chunk 4*h + lane/16 for K-step half h; row % 8 == lane % 8 for every block, so the
+  // swizzled chunk depends on the lane only and each half has one base offset.
+  const int frag_row = lane & 15;
+  const int frag_chunk = lane >> 4;
+  int x_base[2], y_base[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int xrow = wave_n * (C::BN / C::WN) + frag_row;
+    const int yrow = wave_m * (C::BM / C::WM) + frag_row;
+    x_base[h] = xrow * C::BK + swizzle<C>(xrow, 4 * h + frag_chunk) * 16;
+    y_base[h] = C::kXBytes + yrow * C::BK + swizzle<C>(yrow, 4 * h + frag_chunk) * 16;
+  }
+  auto xaddr = [&] __device__(int slot, int h, int i) __attribute__((always_inline)) {
+    return lds + slot * C::kStageBytes + x_base[h] + i * 16 * C::BK;
+  };
+  auto yaddr = [&] __device__(int slot, int h, int j) __attribute__((always_inline)) {
+    return lds + slot * C::kStageBytes + y_base[h] + j * 16 * C::BK;
+  };
+
+  i32x4 acc[C::TM][C::TN];
+#pragma unroll
+  for (int j = 0; j < C::TM; ++j)
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i) acc[j][i] = i32x4{0, 0, 0, 0};
+
+  // Register sets: xf[0] / yf[0..TM-1] hold the fragments of even K-steps (step A),
+  // xf[1] / yf[0..TM-kSpare-1] + ysp[*] those of odd K-steps (step B).
+  constexpr int kMain = C::TM - C::kSpare;
+  i32x4 xf[2][C::TN], yf[C::TM], ysp[C::kSpare];
+  auto debias = [&] __device__(int buf) __attribute__((always_inline)) {
+    if constexpr (kCode == WeightCode::kBiasedU8) {
+#pragma unroll
+      for (int i = 0; i < C::TN; ++i) xf[buf][i] ^= int32_t(0x80808080u);
+    }
+  };
+  // Step A: MFMAs of an even K-step; loads the odd K-step (half 1 of `slot`).
+  auto step_a = [&] __device__(int slot) __attribute__((always_inline)) {
+    debias(0);
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i) xf[1][i] = ld(xaddr(slot, 1, i));
+#pragma unroll
+    for (int s2 = 0; s2 < C::kSpare; ++s2) ysp[s2] = ld(yaddr(slot, 1, kMain + s2));
+#pragma unroll
+    for (int j = 0; j < C::TM; ++j) {
+#pragma unroll
+      for (int i = 0; i < C::TN; ++i) acc[j][i] = mfma16(xf[0][i], yf[j], acc[j][i]);
+      if (j < kMain) yf[j] = ld(yaddr(slot, 1, j));
+    }
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i) {
+      sched_group<0x008, 1>();  // MFMA
+      sched_group<0x100, 1>();  // DS read (W fragment)
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < C::kSpare; ++s2) {
+      sched_group<0x008, 1>();
+      sched_group<0x100, 1>();  // DS read (spare A fragment)
+    }
+    AReloads<0, kMain, C::TM, C::TN, C::TN + C::kSpare>::run();
+  };
+  // Step B: copies of stage t+2, MFMAs of the odd K-step; loads the next even K-step
+  // (half 0 of `next_slot`).
+  auto step_b = [&] __device__(int t, int next_slot) __attribute__((always_inline)) {
+    issue(t + 2);
+    debias(1);
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i) xf[0][i] = ld(xaddr(next_slot, 0, i));
+#pragma unroll
+    for (int s2 = 0; s2 < C::kSpare; ++s2) yf[kMain + s2] = ld(yaddr(next_slot, 0, kMain + s2));
+#pragma unroll
+    for (int j = 0; j < C::TM; ++j) {
+#pragma unroll
+      for (int i = 0; i < C::TN; ++i)
+        acc[j][i] = mfma16(xf[1][i], j < kMain ? yf[j] : ysp[j - kMain], acc[j][i]);
+      if (j < kMain) yf[j] = ld(yaddr(next_slot, 0, j));
+    }
+#pragma unroll
+    for (int i = 0; i < C::kLoads; ++i) {
+      sched_group<0x008, 1>();  // MFMA
+      sched_group<0x010, 1>();  // VMEM (LDS DMA)
+    }
+#pragma unroll
+    for (int i = 0; i < C::TN + C::kSpare; ++i) {
+      sched_group<0x008, 1>();
+      sched_group<0x100, 1>();  // DS read (W fragment, then A fragments 6..7)
+    }
+    AReloads<0, kMain, C::TM, C::TN, C::kLoads + C::TN + C::kSpare>::run();
+  };
+  // Between A and B: own copies of stage t+1 landed, own reads of slot t%2 returned.
+  auto sync = [&] __device__() __attribute__((always_inline)) {
+    waitcnt<vmcnt_imm(0)>();
+    waitcnt<lgkmcnt0_imm()>();
+    workgroup_barrier();
+  };
+
+  issue(0);
+  issue(1);
+  waitcnt<vmcnt_imm(C::kLoads)>();  // stage 0 landed (stage 1 may be in flight)
+  workgroup_barrier();
+#pragma unroll
+  for (int i = 0; i < C::TN; ++i) xf[0][i] = ld(xaddr(0, 0, i));
+#pragma unroll
+  for (int j = 0; j < C::TM; ++j) yf[j] = ld(yaddr(0, 0, j));
+
+  for (int t = 0; t < ns; ++t) {
+    const int slot = t & 1;
+    step_a(slot);
+    sync();
+    step_b(t, slot ^ 1);
+  }
+  waitcnt<vmcnt_imm(0)>();  // padding copies of the last two steps
+#undef CI8_DMA_RSRC
+
+  // Epilogue: lane holds D[n][m] for m = lane % 16 and n = 4 * (lane / 16) + e.
+#pragma unroll
+  for (int j = 0; j < C::TM; ++j) {
+    const int row = m0 + wave_m * (C::BM / C::WM) + j * 16 + frag_row;
+    if (row >= m) continue;
+    const float row_scale = sa[row];
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i) {
+      const int col = n0 + wave_n * (C::BN / C::WN) + i * 16 + frag_chunk * 4;
+      if (col >= n) continue;
+      const int64_t base = int64_t(row) * n + col;
+      if (vec_n) {
+        const u32x2 s2 = *reinterpret_cast<const u32x2*>(sw + col);
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t sbits = (s2[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+          v[e] = (float(acc[j][i][e]) * row_scale) * bf16_to_f32(sbits);
+        }
+        *reinterpret_cast<u32x2*>(out + base) =
+            u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        if constexpr (kWorkspace) *reinterpret_cast<i32x4*>(ws + base) = acc[j][i];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (col + e < n) {
+            const float v = (float(acc[j][i][e]) * row_scale) * bf16_to_f32(sw[col + e]);
+            out[base + e] = uint16_t(f32_to_bf16(v));
+            if constexpr (kWorkspace) ws[base + e] = acc[j][i][e];
+          }
+        }
+      }
+    }
+  }
+}
+
+template <class C, WeightCode kCode, bool kWorkspace, bool kExactK>
+hipError_t run_k128_exact(const int8_t* a, const void* w, const float* sa, const void* sw,
+                          void* out, int32_t* ws, int m, int n, int k, hipStream_t stream) {
+  auto kernel = channel_gemm_k128_kernel<C, kCode, kWorkspace, kExactK>;
+  static bool configured = false;  // benign race: every thread sets the same attribute
+  if (!configured) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             C::kLdsBytes);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  const int blocks = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
+  const bool vec_n = n % 4 == 0 && reinterpret_cast<uintptr_t>(sw) % 8 == 0 &&
+                     reinterpret_cast<uintptr_t>(out) % 8 == 0 &&
+                     reinterpret_cast<uintptr_t>(ws) % 16 == 0;
+  kernel<<<blocks, C::kThreads, C::kLdsBytes, stream>>>(
+      a, w, sa, static_cast<const uint16_t*>(sw), static_cast<uint16_t*>(out), ws, m, n, k,
+      vec_n);
+  return hipGetLastError();
+}
+
+template <class C, WeightCode kCode, bool kWorkspace>
+hipError_t run_k128(const int8_t* a, const void* w, const float* sa, const void* sw, void* out,
+                    int32_t* ws, int m, int n, int k, hipStream_t stream) {
+  if (k % C::BK == 0)
+    return run_k128_exact<C, kCode, kWorkspace, true>(a, w, sa, sw, out, ws, m, n, k, stream);
+  return run_k128_exact<C, kCode, kWorkspace, false>(a, w, sa, sw, out, ws, m, n, k, stream);
+}
+
 // Tile configurations. All produce identical bits; they differ only in speed.
 using Large = TileConfig<256, 256, 64, 2, 2, 3, 8>;   // 4 waves, 128x128 per wave
 using Medium = TileConfig<128, 128, 64, 2, 2, 3, 8>;  // 4 waves, 64x64 per wave
 using Small = TileConfig<256, 32, 128, 4, 1, 2, 1>;   // skinny M: 4 waves stacked on n
+using Pipe224 = K128Config<256, 224, 2, 2, 8>;        // 4 waves, 128x112 per wave
 
 template <WeightCode kCode, bool kWorkspace>
 hipError_t dispatch(const int8_t* a, const void* w, const float* sa, const void* sw, void* out,
@@ -265,8 +621,10 @@ hipError_t dispatch(const int8_t* a, const void* w, const float* sa, const void*
     case 1:
     case 3:
       return run<Medium, kCode, kWorkspace>(a, w, sa, sw, out, ws, m, n, k, stream);
-    default:
+    case 2:
       return run<Large, kCode, kWorkspace>(a, w, sa, sw, out, ws, m, n, k, stream);
+    default:
+      return run_k128<Pipe224, kCode, kWorkspace>(a, w, sa, sw, out, ws, m, n, k, stream);
   }
 }
 
