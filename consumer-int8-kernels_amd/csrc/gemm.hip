@@ -21,6 +21,8 @@
 //  * Workgroup ids are remapped so that consecutive tiles of a grouped raster land on
 //    the same XCD (the hardware deals workgroups round-robin over the 8 XCDs), which
 //    keeps the A and W panels they share in that XCD's L2.
+#include <type_traits>
+
 #include "ci8_device.h"
 #include "launch.h"
 
@@ -62,6 +64,12 @@ struct TileConfig {
 __device__ __forceinline__ i32x4 ld(const char __attribute__((address_space(3)))* p) {
   return *reinterpret_cast<const __attribute__((address_space(3))) i32x4*>(p);
 }
+
+// Keeps the instruction scheduler from moving any instruction across this point. The
+// epilogues use it to keep every scale load ahead of the first store: stores share the
+// vector-memory counter with loads, so a load scheduled after a store makes its wait
+// also wait for that store.
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
 // Chunk slot of logical 16-byte chunk c in LDS row r. A fragment load has 16
 // consecutive lanes reading 16 consecutive rows at the same logical chunk; the XOR
@@ -193,27 +201,39 @@ __global__ void __launch_bounds__(C::kThreads) channel_gemm_kernel(
     }
   }
 
-  // Epilogue. Lane holds D[n][m] for m = lane % 32 and n = 8*r4 + 4*(lane/32) + j.
+  // Epilogue. Lane holds D[n][m] for m = lane % 32 and n = 8*r4 + 4*(lane/32) + e.
   // vec_n: n % 4 == 0 and sw, out (and ws) aligned for 8-byte (16-byte) accesses.
+  // All scale loads precede the first store (stores share the vector-memory counter).
+  float row_scale[C::TM];
 #pragma unroll
   for (int j = 0; j < C::TM; ++j) {
-    const int row = m0 + y_row0 + j * 32 + frag_row;  // output row (m)
-    if (row >= m) continue;
-    const float row_scale = sa[row];
+    const int row = m0 + y_row0 + j * 32 + frag_row;
+    row_scale[j] = row < m ? sa[row] : 0.f;
+  }
+  if (vec_n && m0 + C::BM <= m && n0 + C::BN <= n) {
+    // Whole block tile in bounds (block-uniform test): unguarded stores after one wait.
+    u32x2 s2[C::TN][4];
 #pragma unroll
-    for (int i = 0; i < C::TN; ++i) {
+    for (int i = 0; i < C::TN; ++i)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int col = n0 + x_row0 + i * 32 + r4 * 8 + frag_half * 4;  // output column (n)
-        if (col >= n) continue;
-        const int64_t base = int64_t(row) * n + col;
-        if (vec_n) {
-          const u32x2 s2 = *reinterpret_cast<const u32x2*>(sw + col);
+      for (int r4 = 0; r4 < 4; ++r4)
+        s2[i][r4] = *reinterpret_cast<const u32x2*>(
+            sw + n0 + x_row0 + i * 32 + r4 * 8 + frag_half * 4);
+    sched_fence();
+#pragma unroll
+    for (int j = 0; j < C::TM; ++j) {
+      const int64_t row_base =
+          int64_t(m0 + y_row0 + j * 32 + frag_row) * n + n0 + x_row0 + frag_half * 4;
+#pragma unroll
+      for (int i = 0; i < C::TN; ++i) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int64_t base = row_base + i * 32 + r4 * 8;
           float v[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const uint32_t sbits = (s2[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-            v[e] = (float(acc[i][j][r4 * 4 + e]) * row_scale) * bf16_to_f32(sbits);
+            const uint32_t sbits = (s2[i][r4][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+            v[e] = (float(acc[i][j][r4 * 4 + e]) * row_scale[j]) * bf16_to_f32(sbits);
           }
           *reinterpret_cast<u32x2*>(out + base) = u32x2{pack_bf16x2(v[0], v[1]),
                                                          pack_bf16x2(v[2], v[3])};
@@ -221,18 +241,70 @@ __global__ void __launch_bounds__(C::kThreads) channel_gemm_kernel(
             *reinterpret_cast<i32x4*>(ws + base) =
                 i32x4{acc[i][j][r4 * 4 + 0], acc[i][j][r4 * 4 + 1], acc[i][j][r4 * 4 + 2],
                       acc[i][j][r4 * 4 + 3]};
-        } else {
+        }
+      }
+    }
+  } else if (vec_n) {
+    u32x2 s2[C::TN][4];
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int col = n0 + x_row0 + i * 32 + r4 * 8 + frag_half * 4;
+        s2[i][r4] = col < n ? *reinterpret_cast<const u32x2*>(sw + col) : u32x2{0, 0};
+      }
+    sched_fence();
+#pragma unroll
+    for (int j = 0; j < C::TM; ++j) {
+      const int row = m0 + y_row0 + j * 32 + frag_row;  // output row (m)
+      if (row >= m) continue;
+#pragma unroll
+      for (int i = 0; i < C::TN; ++i) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int col = n0 + x_row0 + i * 32 + r4 * 8 + frag_half * 4;  // output column (n)
+          if (col >= n) continue;
+          const int64_t base = int64_t(row) * n + col;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t sbits = (s2[i][r4][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+            v[e] = (float(acc[i][j][r4 * 4 + e]) * row_scale[j]) * bf16_to_f32(sbits);
+          }
+          *reinterpret_cast<u32x2*>(out + base) = u32x2{pack_bf16x2(v[0], v[1]),
+                                                         pack_bf16x2(v[2], v[3])};
+          if constexpr (kWorkspace)
+            *reinterpret_cast<i32x4*>(ws + base) =
+                i32x4{acc[i][j][r4 * 4 + 0], acc[i][j][r4 * 4 + 1], acc[i][j][r4 * 4 + 2],
+                      acc[i][j][r4 * 4 + 3]};
+        }
+      }
+    }
+  } else {
+    // Element stores, column group by column group (scales loaded before its stores).
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int col = n0 + x_row0 + i * 32 + r4 * 8 + frag_half * 4;
+        float sc[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[e] = col + e < n ? bf16_to_f32(sw[col + e]) : 0.f;
+#pragma unroll
+        for (int j = 0; j < C::TM; ++j) {
+          const int row = m0 + y_row0 + j * 32 + frag_row;
+          if (row >= m) continue;
+          const int64_t base = int64_t(row) * n + col;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             if (col + e < n) {
-              const float v = (float(acc[i][j][r4 * 4 + e]) * row_scale) * bf16_to_f32(sw[col + e]);
-              out[base + e] = uint16_t(f32_to_bf16(v));
+              out[base + e] =
+                  uint16_t(f32_to_bf16((float(acc[i][j][r4 * 4 + e]) * row_scale[j]) * sc[e]));
               if constexpr (kWorkspace) ws[base + e] = acc[i][j][r4 * 4 + e];
             }
           }
         }
       }
-    }
   }
 }
 
@@ -256,6 +328,102 @@ hipError_t run(const int8_t* a, const void* w, const float* sa, const void* sw, 
       a, w, sa, static_cast<const uint16_t*>(sw), static_cast<uint16_t*>(out), ws, m, n, k,
       vec_n);
   return hipGetLastError();
+}
+
+// Epilogue for accumulators in the 16x16 MFMA layout: lane holds D[n][m] for
+// m = lane % 16 and n = 4 * (lane / 16) + e of each block. All scale loads are issued
+// before the first store: on gfx9 stores share the vector-memory counter with loads, so
+// a load issued after a store cannot be waited for without also waiting for the store.
+template <int TM, int TN, bool kWorkspace>
+__device__ __forceinline__ void store_tile16(const i32x4 (&acc)[TM][TN], int row0, int col0,
+                                             int m, int n, const float* __restrict__ sa,
+                                             const uint16_t* __restrict__ sw,
+                                             uint16_t* __restrict__ out, int32_t* __restrict__ ws,
+                                             bool vec_n) {
+  const int lane = threadIdx.x & 63;
+  const int frag_row = lane & 15, frag_group = lane >> 4;
+  float row_scale[TM];
+#pragma unroll
+  for (int j = 0; j < TM; ++j) {
+    const int row = row0 + j * 16 + frag_row;
+    row_scale[j] = row < m ? sa[row] : 0.f;
+  }
+  if (vec_n && row0 + TM * 16 <= m && col0 + TN * 16 <= n) {
+    // Whole wave tile in bounds (wave-uniform test): no per-element guards, so the
+    // stores are issued back to back after a single wait for the scale loads.
+    u32x2 s2[TN];
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+      s2[i] = *reinterpret_cast<const u32x2*>(sw + col0 + i * 16 + frag_group * 4);
+    sched_fence();
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+      const int64_t row_base = int64_t(row0 + j * 16 + frag_row) * n + col0 + frag_group * 4;
+#pragma unroll
+      for (int i = 0; i < TN; ++i) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t sbits = (s2[i][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+          v[e] = (float(acc[j][i][e]) * row_scale[j]) * bf16_to_f32(sbits);
+        }
+        *reinterpret_cast<u32x2*>(out + row_base + i * 16) =
+            u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        if constexpr (kWorkspace) *reinterpret_cast<i32x4*>(ws + row_base + i * 16) = acc[j][i];
+      }
+    }
+  } else if (vec_n) {
+    u32x2 s2[TN];
+#pragma unroll
+    for (int i = 0; i < TN; ++i) {
+      const int col = col0 + i * 16 + frag_group * 4;
+      s2[i] = col < n ? *reinterpret_cast<const u32x2*>(sw + col) : u32x2{0, 0};
+    }
+    sched_fence();
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+      const int row = row0 + j * 16 + frag_row;
+      if (row >= m) continue;
+#pragma unroll
+      for (int i = 0; i < TN; ++i) {
+        const int col = col0 + i * 16 + frag_group * 4;
+        if (col >= n) continue;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t sbits = (s2[i][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+          v[e] = (float(acc[j][i][e]) * row_scale[j]) * bf16_to_f32(sbits);
+        }
+        const int64_t base = int64_t(row) * n + col;
+        *reinterpret_cast<u32x2*>(out + base) =
+            u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        if constexpr (kWorkspace) *reinterpret_cast<i32x4*>(ws + base) = acc[j][i];
+      }
+    }
+  } else {
+    // Unaligned or n % 4 != 0 (channel_mm accepts any n): element stores, column block
+    // by column block, each block's four scales loaded before its stores.
+#pragma unroll
+    for (int i = 0; i < TN; ++i) {
+      const int col = col0 + i * 16 + frag_group * 4;
+      float sc[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sc[e] = col + e < n ? bf16_to_f32(sw[col + e]) : 0.f;
+#pragma unroll
+      for (int j = 0; j < TM; ++j) {
+        const int row = row0 + j * 16 + frag_row;
+        if (row >= m) continue;
+        const int64_t base = int64_t(row) * n + col;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (col + e < n) {
+            out[base + e] = uint16_t(f32_to_bf16((float(acc[j][i][e]) * row_scale[j]) * sc[e]));
+            if constexpr (kWorkspace) ws[base + e] = acc[j][i][e];
+          }
+        }
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------
@@ -313,6 +481,10 @@ struct K128Config {
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, lds_void* dst, uint32_t voffset,
                                       int soffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, voffset, soffset, 0, 0);
+}
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset,
+                                               int soffset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voffset, soffset, 0));
 }
 template <int kImm>
 __device__ __forceinline__ void waitcnt() {
@@ -538,40 +710,272 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_k128_kernel(
   waitcnt<vmcnt_imm(0)>();  // padding copies of the last two steps
 #undef CI8_DMA_RSRC
 
-  // Epilogue: lane holds D[n][m] for m = lane % 16 and n = 4 * (lane / 16) + e.
+  store_tile16<C::TM, C::TN, kWorkspace>(acc, m0 + wave_m * (C::BM / C::WM),
+                                        n0 + wave_n * (C::BN / C::WN), m, n, sa, sw, out, ws,
+                                        vec_n);
+}
+
+// ---------------------------------------------------------------------------------
+// Large-tile kernel with W staged in LDS and A loaded straight into registers.
+//
+// Tile 256(m) x 224(n); the four waves are stacked along m, each owning 64 rows x 224
+// columns as 4 x 14 16x16 INT32 accumulators (224 AGPRs). A wave's A rows are private
+// to it, so they are loaded from L2 directly into the MFMA operand registers (no LDS,
+// no sharing, no extra traffic), while the 224 W rows, used by all four waves, go
+// through an LDS ring filled by buffer_load ... lds. With only W in LDS a stage of 128
+// K-bytes is 28 KB, so a ring of four slots keeps three stages in flight, and the A
+// loads of the next stage are in flight in a second register set: about 116 KB of
+// operands in flight per CU (twice what fits when both operands share LDS).
+//
+// K order: within a 128-byte stage, MFMA lane group g (lane / 16) takes physical chunk
+// 2g + h in K-step h (0 or 1). A and W use the same order, so the dot products are
+// unchanged, and each lane's two 16-byte A loads per block cover a whole 128-byte line
+// of its row.
+//
+// For stage t (K-steps h = 0, 1), each wave:
+//   h = 0: issue the A loads of stage t+1 (into the other register set); 56 MFMAs;
+//          reload each W fragment for K-step (t, 1) right after its last MFMA;
+//   sync:  own W copies of stage t+1 landed, then a barrier (all waves' copies landed;
+//          every wave finished K-step (t, 0), so nobody reads the slot of stage t-1);
+//   h = 1: issue the W copies of stage t+3 into the slot of stage t-1; 56 MFMAs;
+//          reload the W fragments for K-step (t+1, 0).
+template <int BN_, int GROUP_M_>
+struct WLdsConfig {
+  static constexpr int BM = 256, BN = BN_, GROUP_M = GROUP_M_;
+  static constexpr int BK = 128;        // K bytes per stage (two 64-deep MFMA steps)
+  static constexpr int kWaves = 4;      // stacked along m
+  static constexpr int kThreads = 256;
+  static constexpr int TM = BM / kWaves / 16;  // 16-row m blocks per wave (4)
+  static constexpr int TN = BN / 16;           // 16-row n blocks per wave
+  static constexpr int kSlots = 4;             // W ring (a power of two: cheap slot math)
+  static constexpr int kAhead = kSlots - 1;    // W stages in flight
+  static constexpr int kChunksPerRow = BK / 16;
+  static constexpr int kStageBytes = BN * BK;
+  static constexpr int kBlocks = kStageBytes / 1024;
+  static constexpr int kLoads = kBlocks / kWaves;  // W DMA per wave per stage
+  static constexpr int kLdsBytes = kSlots * kStageBytes;
+  static_assert(kLoads * kWaves == kBlocks, "whole 1 KiB W blocks per wave");
+  static_assert(TM * 16 * kWaves == BM && TN * 16 == BN, "wave tiling");
+  static_assert(kLdsBytes <= 160 * 1024, "LDS");
+};
+
+template <class C, WeightCode kCode, bool kWorkspace, bool kExactK>
+__global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
+    const int8_t* __restrict__ a, const void* __restrict__ w, const float* __restrict__ sa,
+    const uint16_t* __restrict__ sw, uint16_t* __restrict__ out, int32_t* __restrict__ ws,
+    int m, int n, int k, bool vec_n) {
+  extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
+  auto* lds = (char __attribute__((address_space(3)))*)(lds_raw);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+
+  const int tiles_n = (n + C::BN - 1) / C::BN;
+  const int tiles_m = (m + C::BM - 1) / C::BM;
+  const int blocks = tiles_n * tiles_m;
+  int logical = blockIdx.x;
+  {
+    const int per = blocks / kXcds, extra = blocks % kXcds;
+    const int xcd = logical % kXcds, idx = logical / kXcds;
+    logical = (xcd < extra ? xcd * (per + 1) : extra * (per + 1) + (xcd - extra) * per) + idx;
+  }
+  const int group_span = C::GROUP_M * tiles_n;
+  const int first_m = (logical / group_span) * C::GROUP_M;
+  const int group_rows = min(tiles_m - first_m, C::GROUP_M);
+  const int tile_m = first_m + (logical % group_span) % group_rows;
+  const int tile_n = (logical % group_span) / group_rows;
+  const int n0 = tile_n * C::BN, m0 = tile_m * C::BM;
+
+  const auto w_rsrc = make_rsrc(w, uint32_t(n) * uint32_t(k));
+  const auto a_rsrc = make_rsrc(a, uint32_t(m) * uint32_t(k));
+  const int ns = (k + C::BK - 1) / C::BK;  // stages
+
+  // W copies: this wave's kLoads 1 KiB blocks of a stage (8 rows x 128 bytes each).
+  uint32_t dma_base[C::kLoads];
+  int dma_col[C::kLoads];
 #pragma unroll
-  for (int j = 0; j < C::TM; ++j) {
-    const int row = m0 + wave_m * (C::BM / C::WM) + j * 16 + frag_row;
-    if (row >= m) continue;
-    const float row_scale = sa[row];
+  for (int i = 0; i < C::kLoads; ++i) {
+    const int block = i * C::kWaves + wave;
+    const int q = block * 64 + lane;
+    const int row = q / C::kChunksPerRow;
+    const int chunk = swizzle<C>(row, q % C::kChunksPerRow);  // the swizzle is an involution
+    const int grow = n0 + row;
+    dma_col[i] = chunk * 16;
+    dma_base[i] = grow < n ? uint32_t(grow) * uint32_t(k) + uint32_t(chunk * 16) : kOutOfRange;
+  }
+  // Stages past the end re-read stage 0 into a slot nobody reads again.
+  auto issue_w = [&] __device__(int t) __attribute__((always_inline)) {
+    const int st = t < ns ? t : 0;
+    auto* slot = lds + (t & (C::kSlots - 1)) * C::kStageBytes;
+    if constexpr (kExactK) {
 #pragma unroll
-    for (int i = 0; i < C::TN; ++i) {
-      const int col = n0 + wave_n * (C::BN / C::WN) + i * 16 + frag_chunk * 4;
-      if (col >= n) continue;
-      const int64_t base = int64_t(row) * n + col;
-      if (vec_n) {
-        const u32x2 s2 = *reinterpret_cast<const u32x2*>(sw + col);
-        float v[4];
+      for (int i = 0; i < C::kLoads; ++i)
+        dma16(w_rsrc, reinterpret_cast<lds_void*>(slot + (i * C::kWaves + wave) * 1024),
+              dma_base[i], st * C::BK);
+    } else {
+      const int k0 = st * C::BK;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t sbits = (s2[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-          v[e] = (float(acc[j][i][e]) * row_scale) * bf16_to_f32(sbits);
-        }
-        *reinterpret_cast<u32x2*>(out + base) =
-            u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-        if constexpr (kWorkspace) *reinterpret_cast<i32x4*>(ws + base) = acc[j][i];
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (col + e < n) {
-            const float v = (float(acc[j][i][e]) * row_scale) * bf16_to_f32(sw[col + e]);
-            out[base + e] = uint16_t(f32_to_bf16(v));
-            if constexpr (kWorkspace) ws[base + e] = acc[j][i][e];
-          }
-        }
+      for (int i = 0; i < C::kLoads; ++i) {
+        const bool live = dma_base[i] != kOutOfRange && k0 + dma_col[i] < k;
+        dma16(w_rsrc, reinterpret_cast<lds_void*>(slot + (i * C::kWaves + wave) * 1024),
+              live ? dma_base[i] + uint32_t(k0) : kOutOfRange, 0);
       }
     }
+  };
+
+  // A loads: block j, K-step h -> 16 bytes of row (lane % 16) at chunk 2 * (lane / 16) + h.
+  const int frag_row = lane & 15;
+  const int frag_group = lane >> 4;
+  const int a_row0 = m0 + wave * (C::BM / C::kWaves) + frag_row;
+  // Per-lane voffsets (the stage's K offset goes in the scalar soffset); rows past m
+  // start out of range and stay out of range whatever soffset is added.
+  uint32_t a_voff[C::TM][2];
+#pragma unroll
+  for (int j = 0; j < C::TM; ++j) {
+    const int row = a_row0 + j * 16;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      a_voff[j][h] = row < m ? uint32_t(row) * uint32_t(k) + uint32_t(frag_group * 32 + h * 16)
+                             : kOutOfRange;
   }
+  i32x4 af[2][2][C::TM];  // [register set][K-step][m block]
+  auto load_a = [&] __device__(int t, int set) __attribute__((always_inline)) {
+    const int st = t < ns ? t : 0;
+    const int k0 = st * C::BK;
+#pragma unroll
+    for (int j = 0; j < C::TM; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if constexpr (kExactK) {
+          af[set][h][j] = __builtin_bit_cast(i32x4, buffer_load16(a_rsrc, a_voff[j][h], k0));
+        } else {
+          const bool live = a_voff[j][h] != kOutOfRange && k0 + frag_group * 32 + h * 16 < k;
+          af[set][h][j] = __builtin_bit_cast(
+              i32x4, buffer_load16(a_rsrc, live ? a_voff[j][h] + uint32_t(k0) : kOutOfRange, 0));
+        }
+      }
+  };
+
+  // W fragments: row (lane % 16) of each 16-row block, chunk 2 * (lane / 16) + h; the
+  // swizzle depends on row % 8 == lane % 8 only, so each K-step half has one base.
+  int x_base[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) x_base[h] = frag_row * C::BK + swizzle<C>(frag_row, 2 * frag_group + h) * 16;
+  auto xaddr = [&] __device__(int t, int h, int i) __attribute__((always_inline)) {
+    return lds + (t & (C::kSlots - 1)) * C::kStageBytes + x_base[h] + i * 16 * C::BK;
+  };
+
+  i32x4 acc[C::TM][C::TN];
+#pragma unroll
+  for (int j = 0; j < C::TM; ++j)
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i) acc[j][i] = i32x4{0, 0, 0, 0};
+  i32x4 xf[C::TN];
+
+  // One K-step: MFMAs with the W fragments in xf and A set `set`, K-step h; each W
+  // fragment is reloaded for K-step (nt, nh) after its last MFMA.
+  auto kstep = [&] __device__(int set, int h, int nt, int nh) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i) {
+      i32x4 x = xf[i];
+      if constexpr (kCode == WeightCode::kBiasedU8) x ^= int32_t(0x80808080u);
+#pragma unroll
+      for (int j = 0; j < C::TM; ++j) acc[j][i] = mfma16(x, af[set][h][j], acc[j][i]);
+      xf[i] = ld(xaddr(nt, nh, i));
+    }
+  };
+  // Scheduling: the K-step's VMEM instructions alternate with its first MFMAs (which
+  // cover W fragments 0 and 1), then each W fragment reload follows its group of TM
+  // MFMAs.
+  auto sched_kstep = [&] __device__(auto vmem_mask, auto vmem_count) __attribute__((always_inline)) {
+    constexpr int kVmem = decltype(vmem_count)::value;
+    static_assert(kVmem <= 2 * C::TM, "VMEM instructions fit in the first two groups");
+#pragma unroll
+    for (int i = 0; i < kVmem; ++i) {
+      sched_group<0x008, 1>();
+      sched_group<decltype(vmem_mask)::value, 1>();
+    }
+    if constexpr (2 * C::TM > kVmem) sched_group<0x008, 2 * C::TM - kVmem>();
+    sched_group<0x100, 2>();  // W fragments 0, 1
+#pragma unroll
+    for (int i = 2; i < C::TN; ++i) {
+      sched_group<0x008, C::TM>();
+      sched_group<0x100, 1>();
+    }
+  };
+  // Before K-step (t, 1): own W copies of stage t+1 landed. Vector-memory operations
+  // are counted in issue order; after those copies this wave issued the copies of
+  // stages t+2 .. t+kAhead-1 and the A loads of stages t (steady state only; already
+  // consumed by K-step (t, 0)) and t+1, so allowing the last two groups outstanding
+  // guarantees stage t+1 (and is exact for t = 0, where the prologue issued W copies
+  // 0..kAhead-1 before A stage 1).
+  auto sync = [&] __device__() __attribute__((always_inline)) {
+    waitcnt<vmcnt_imm((C::kAhead - 2) * C::kLoads + 2 * C::TM)>();
+    workgroup_barrier();
+  };
+  auto stage = [&] __device__(int t, int set) __attribute__((always_inline)) {
+    load_a(t + 1, set ^ 1);
+    kstep(set, 0, t, 1);
+    sched_kstep(std::integral_constant<int, 0x020>{}, std::integral_constant<int, 2 * C::TM>{});
+    sync();
+    issue_w(t + C::kAhead);
+    kstep(set, 1, t + 1, 0);
+    sched_kstep(std::integral_constant<int, 0x010>{}, std::integral_constant<int, C::kLoads>{});
+  };
+
+  // Prologue: W stages 0..kAhead-1 and A stage 0; the W fragments of K-step (0, 0).
+  // Issue order matters: the compiler's vector-memory counter tracking at the loop head
+  // merges this prologue's state, so A stage 0 must precede the later W copies.
+  issue_w(0);
+  load_a(0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int t = 1; t < C::kAhead; ++t) issue_w(t);
+  waitcnt<vmcnt_imm((C::kAhead - 1) * C::kLoads)>();  // W stage 0 and A stage 0 landed
+  workgroup_barrier();
+#pragma unroll
+  for (int i = 0; i < C::TN; ++i) xf[i] = ld(xaddr(0, 0, i));
+
+  int t = 0;
+  for (; t + 1 < ns; t += 2) {
+    stage(t, 0);
+    stage(t + 1, 1);
+  }
+  if (t < ns) stage(t, 0);
+  waitcnt<vmcnt_imm(0)>();  // copies past the last stage
+
+  store_tile16<C::TM, C::TN, kWorkspace>(acc, m0 + wave * (C::BM / C::kWaves), n0, m, n, sa, sw,
+                                        out, ws, vec_n);
+}
+
+template <class C, WeightCode kCode, bool kWorkspace, bool kExactK>
+hipError_t run_wlds_exact(const int8_t* a, const void* w, const float* sa, const void* sw,
+                          void* out, int32_t* ws, int m, int n, int k, hipStream_t stream) {
+  auto kernel = channel_gemm_wlds_kernel<C, kCode, kWorkspace, kExactK>;
+  static bool configured = false;  // benign race: every thread sets the same attribute
+  if (!configured) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             C::kLdsBytes);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  const int blocks = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
+  const bool vec_n = n % 4 == 0 && reinterpret_cast<uintptr_t>(sw) % 8 == 0 &&
+                     reinterpret_cast<uintptr_t>(out) % 8 == 0 &&
+                     reinterpret_cast<uintptr_t>(ws) % 16 == 0;
+  kernel<<<blocks, C::kThreads, C::kLdsBytes, stream>>>(
+      a, w, sa, static_cast<const uint16_t*>(sw), static_cast<uint16_t*>(out), ws, m, n, k,
+      vec_n);
+  return hipGetLastError();
+}
+
+template <class C, WeightCode kCode, bool kWorkspace>
+hipError_t run_wlds(const int8_t* a, const void* w, const float* sa, const void* sw, void* out,
+                    int32_t* ws, int m, int n, int k, hipStream_t stream) {
+  if (k % C::BK == 0)
+    return run_wlds_exact<C, kCode, kWorkspace, true>(a, w, sa, sw, out, ws, m, n, k, stream);
+  return run_wlds_exact<C, kCode, kWorkspace, false>(a, w, sa, sw, out, ws, m, n, k, stream);
 }
 
 template <class C, WeightCode kCode, bool kWorkspace, bool kExactK>
@@ -609,6 +1013,7 @@ using Large = TileConfig<256, 256, 64, 2, 2, 3, 8>;   // 4 waves, 128x128 per wa
 using Medium = TileConfig<128, 128, 64, 2, 2, 3, 8>;  // 4 waves, 64x64 per wave
 using Small = TileConfig<256, 32, 128, 4, 1, 2, 1>;   // skinny M: 4 waves stacked on n
 using Pipe224 = K128Config<256, 224, 2, 2, 8>;        // 4 waves, 128x112 per wave
+using WLds224 = WLdsConfig<224, 8>;                   // 4 waves, 64x224 per wave
 
 template <WeightCode kCode, bool kWorkspace>
 hipError_t dispatch(const int8_t* a, const void* w, const float* sa, const void* sw, void* out,
@@ -624,6 +1029,8 @@ hipError_t dispatch(const int8_t* a, const void* w, const float* sa, const void*
     case 2:
       return run<Large, kCode, kWorkspace>(a, w, sa, sw, out, ws, m, n, k, stream);
     default:
+      return run_wlds<WLds224, kCode, kWorkspace>(a, w, sa, sw, out, ws, m, n, k, stream);
+    case 6:
       return run_k128<Pipe224, kCode, kWorkspace>(a, w, sa, sw, out, ws, m, n, k, stream);
   }
 }
