@@ -14,6 +14,7 @@ extra roofline lines, and `cpu_baseline`, the CPU oracle on a bounded row slice 
 same workload on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-extras]
+                      [--copy-calibration]
 """
 
 from __future__ import annotations
@@ -37,6 +38,11 @@ QUANT_BYTES = 3 * M * K + 4 * M  # BF16 read + INT8 write + FP32 scales
 PEAK_INT8_TOPS = 256 * 2.4e9 * 8192 / 1e12  # 5033.2: 256 CUs x 2.4 GHz x 8192 op/clk/CU
 PEAK_HBM_GBS = 8000.0
 GEMV_K, GEMV_N = 5120, 17408
+# HBM-side bytes per GEMM launch at this shape, from two rocprofv3 --pmc runs of this
+# script (FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00; the factors make a plain 512 MiB copy
+# read back its own size). Counters cannot be read from inside a timed run, so the value
+# is carried here and re-measured whenever the GEMM kernel changes.
+GEMM_TRAFFIC_BYTES = 804_800_000
 
 
 def gemv_bytes(m: int) -> int:
@@ -52,6 +58,9 @@ def parse_args():
     p.add_argument("--no-extras", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="approximate CPU time budget of the cpu_baseline sample")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="also run a plain 512 MiB device copy three times (a kernel of known "
+                        "traffic that scales FETCH_SIZE / WRITE_SIZE counters)")
     return p.parse_args()
 
 
@@ -203,7 +212,8 @@ def main() -> int:
             "peak": round(peak_tops, 1),
             "unit": "TFLOP/s",
             "frac": round(gemm_tops / peak_tops, 4),
-            "traffic": None,
+            "traffic": GEMM_TRAFFIC_BYTES,
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (calibrated by a copy)",
             "mean_us": round(gemm_mean_us, 2),
             "median_us": round(statistics.median(gemm_us), 2),
             "ops_per_launch": GEMM_OPS,
@@ -242,6 +252,15 @@ def main() -> int:
                                             "frac": round(gbs / PEAK_HBM_GBS, 4),
                                             "mean_us": round(mean_us, 2), "bytes": gemv_bytes(m)}
         result["extras"] = extras
+
+    if args.copy_calibration:
+        src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        result["copy_calibration_bytes"] = src.numel()
+        del src, dst
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
