@@ -21,6 +21,11 @@ channel_mm(a, w, a_scale, w_scale, out)
     As fused_channel_mm with biased UINT8 weights (signed code + 128).
 channel_gemv(x, w, scale, out)
     W8A16 for 1 <= M <= 16: out = bf16(x @ bf16(w * scale[:, None]).T), FP32 accumulation.
+grouped_summed_mm(a, w, a_scale, w_scale, out)
+    Grouped W8A8 (no reference op; the summed variant of configs[4]): a INT8 [G,M,K]
+    (quantize_grouped4096's codes), w INT8 [G,N,K], a_scale FP32 [G,M], w_scale BF16 [N];
+    out = bf16(sum over ascending g of (float(a[g] @ w[g].T) * a_scale[g, :, None])
+    * w_scale[None, :]), each term rounded to FP32 and summed in FP32.
 """
 
 import torch
@@ -33,6 +38,7 @@ channel_mm = torch.ops.consumer_int8.channel_mm
 channel_gemv = torch.ops.consumer_int8.channel_gemv
 cutlass_channel_mm = torch.ops.consumer_int8.cutlass_channel_mm
 fused_channel_mm = torch.ops.consumer_int8.fused_channel_mm
+grouped_summed_mm = torch.ops.consumer_int8.grouped_summed_mm
 
 
 @torch.library.register_fake("consumer_int8::fused_channel_mm")
@@ -62,4 +68,9 @@ def _channel_gemv_fake(x, w, scale, out):
 
 @torch.library.register_fake("consumer_int8::cutlass_channel_mm")
 def _cutlass_channel_mm_fake(a, w, a_scale, w_scale, workspace, out):
+    return None
+
+
+@torch.library.register_fake("consumer_int8::grouped_summed_mm")
+def _grouped_summed_mm_fake(a, w, a_scale, w_scale, out):
     return None

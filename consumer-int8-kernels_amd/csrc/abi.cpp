@@ -130,6 +130,21 @@ int ci8_channel_mm(const int8_t* a, const uint8_t* w_u8, const float* a_scale,
                                            as_stream(stream)));
 }
 
+int ci8_grouped_summed_mm(const int8_t* a, const int8_t* w, const float* a_scale,
+                          const void* w_scale, void* out, int64_t groups, int64_t m,
+                          int64_t n, int64_t k, void* stream) {
+  if (groups <= 0) return fail(CI8_ERR_GEOMETRY, "Invalid grouped GEMM geometry");
+  const int status = check_gemm(m, n, k, true, "Invalid grouped GEMM geometry");
+  if (status != CI8_OK) return status;
+  if (groups * m > INT_MAX || groups > 65536)
+    return fail(CI8_ERR_TOO_LARGE, "Matrix too large");
+  if (!aligned(a, 16) || !aligned(w, 16) || !aligned(a_scale, 4) || !aligned(w_scale, 2) ||
+      !aligned(out, 2))
+    return fail(CI8_ERR_ALIGNMENT, "grouped_summed_mm requires aligned buffers");
+  return launched(ci8::launch_grouped_summed_gemm(a, w, a_scale, w_scale, out, int(groups),
+                                                  int(m), int(n), int(k), as_stream(stream)));
+}
+
 int ci8_channel_gemv(const void* x, const int8_t* w, const void* scale, void* out, int64_t m,
                      int64_t n, int64_t k, void* stream) {
   if (!(m > 0 && m <= 16 && n > 0 && k > 0 && k <= 65536 && k % 16 == 0))

@@ -104,44 +104,18 @@ __device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rsrc, lds_void*
   }
 }
 
-template <class C, WeightCode kCode, bool kWorkspace>
-__global__ void __launch_bounds__(C::kThreads) channel_gemm_kernel(
-    const int8_t* __restrict__ a, const void* __restrict__ w, const float* __restrict__ sa,
-    const uint16_t* __restrict__ sw, uint16_t* __restrict__ out, int32_t* __restrict__ ws,
-    int m, int n, int k, bool vec_n) {
-  extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
-  auto* lds = (char __attribute__((address_space(3)))*)(lds_raw);
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
-  const int wave_n = wave / C::WM;
-  const int wave_m = wave % C::WM;
-
-  // Workgroup -> tile: undo the round-robin XCD dealing, then a grouped raster.
-  const int tiles_n = (n + C::BN - 1) / C::BN;
-  const int tiles_m = (m + C::BM - 1) / C::BM;
-  const int blocks = tiles_n * tiles_m;
-  int logical = blockIdx.x;
-  {
-    const int per = blocks / kXcds, extra = blocks % kXcds;
-    const int xcd = logical % kXcds, idx = logical / kXcds;
-    logical = (xcd < extra ? xcd * (per + 1) : extra * (per + 1) + (xcd - extra) * per) + idx;
-  }
-  const int group_span = C::GROUP_M * tiles_n;
-  const int first_m = (logical / group_span) * C::GROUP_M;
-  const int group_rows = min(tiles_m - first_m, C::GROUP_M);
-  const int tile_m = first_m + (logical % group_span) % group_rows;
-  const int tile_n = (logical % group_span) / group_rows;
-  const int n0 = tile_n * C::BN, m0 = tile_m * C::BM;
-
+// K loop of the 32x32 kernel: acc += W[n0:n0+BN, :k] . A[m0:m0+BM, :k]^T (as D[n][m])
+// through an STAGES-deep LDS ring. Returns with every vector-memory copy landed; this
+// wave's last LDS reads have been consumed by its MFMAs, but other waves may still be
+// reading the last stage, so a caller that reuses the ring must barrier first.
+template <class C, WeightCode kCode>
+__device__ __forceinline__ void gemm_kloop(i32x16 (&acc)[C::TN][C::TM], const int8_t* a,
+                                           const void* w,
+                                           char __attribute__((address_space(3)))* lds,
+                                           int wave, int lane, int wave_n, int wave_m, int m0,
+                                           int n0, int m, int n, int k) {
   const auto w_rsrc = make_rsrc(w, uint32_t(n) * uint32_t(k));
   const auto a_rsrc = make_rsrc(a, uint32_t(m) * uint32_t(k));
-
-  i32x16 acc[C::TN][C::TM];
-#pragma unroll
-  for (int i = 0; i < C::TN; ++i)
-#pragma unroll
-    for (int j = 0; j < C::TM; ++j) acc[i][j] = i32x16{};
 
   const int nk = (k + C::BK - 1) / C::BK;
   auto issue = [&](int kt) {
@@ -155,7 +129,6 @@ __global__ void __launch_bounds__(C::kThreads) channel_gemm_kernel(
   for (int s = 0; s < C::STAGES - 1; ++s)
     if (s < nk) issue(s);
 
-  // Per-lane fragment geometry: MFMA row/col = lane % 32, K half = lane / 32.
   const int frag_row = lane & 31;
   const int frag_half = lane >> 5;
   const int x_row0 = wave_n * (C::BN / C::WN);
@@ -200,6 +173,51 @@ __global__ void __launch_bounds__(C::kThreads) channel_gemm_kernel(
           acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xf[i], yf[j], acc[i][j], 0, 0, 0);
     }
   }
+
+}
+
+template <class C, WeightCode kCode, bool kWorkspace>
+__global__ void __launch_bounds__(C::kThreads) channel_gemm_kernel(
+    const int8_t* __restrict__ a, const void* __restrict__ w, const float* __restrict__ sa,
+    const uint16_t* __restrict__ sw, uint16_t* __restrict__ out, int32_t* __restrict__ ws,
+    int m, int n, int k, bool vec_n) {
+  extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
+  auto* lds = (char __attribute__((address_space(3)))*)(lds_raw);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+  const int wave_n = wave / C::WM;
+  const int wave_m = wave % C::WM;
+
+  // Workgroup -> tile: undo the round-robin XCD dealing, then a grouped raster.
+  const int tiles_n = (n + C::BN - 1) / C::BN;
+  const int tiles_m = (m + C::BM - 1) / C::BM;
+  const int blocks = tiles_n * tiles_m;
+  int logical = blockIdx.x;
+  {
+    const int per = blocks / kXcds, extra = blocks % kXcds;
+    const int xcd = logical % kXcds, idx = logical / kXcds;
+    logical = (xcd < extra ? xcd * (per + 1) : extra * (per + 1) + (xcd - extra) * per) + idx;
+  }
+  const int group_span = C::GROUP_M * tiles_n;
+  const int first_m = (logical / group_span) * C::GROUP_M;
+  const int group_rows = min(tiles_m - first_m, C::GROUP_M);
+  const int tile_m = first_m + (logical % group_span) % group_rows;
+  const int tile_n = (logical % group_span) / group_rows;
+  const int n0 = tile_n * C::BN, m0 = tile_m * C::BM;
+
+  i32x16 acc[C::TN][C::TM];
+#pragma unroll
+  for (int i = 0; i < C::TN; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TM; ++j) acc[i][j] = i32x16{};
+  gemm_kloop<C, kCode>(acc, a, w, lds, wave, lane, wave_n, wave_m, m0, n0, m, n, k);
+
+  // Per-lane fragment geometry: MFMA row/col = lane % 32, K half = lane / 32.
+  const int frag_row = lane & 31;
+  const int frag_half = lane >> 5;
+  const int x_row0 = wave_n * (C::BN / C::WN);
+  const int y_row0 = wave_m * (C::BM / C::WM);
 
   // Epilogue. Lane holds D[n][m] for m = lane % 32 and n = 8*r4 + 4*(lane/32) + e.
   // vec_n: n % 4 == 0 and sw, out (and ws) aligned for 8-byte (16-byte) accesses.
@@ -1035,6 +1053,139 @@ hipError_t dispatch(const int8_t* a, const void* w, const float* sa, const void*
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Grouped W8A8 with the per-group partials scaled and summed:
+//   out[m, n] = bf16_rn( t_0 + t_1 + ... + t_{G-1} ),  FP32 additions left to right,
+//   t_g = fl( fl( float_rn(acc_g[m, n]) * sa[g, m] ) * float(sw[n]) ),
+//   acc_g = A_g[m, :] . W_g[n, :]  (exact INT32), A [G, M, K], W [G, N, K], sa [G, M].
+// Each term is the fused_channel_mm epilogue of one group; the FP32 sum of scaled INT32
+// partials follows benchmarks/cuda/q8_block_int8.cu:54-55 (the reference has no such
+// op). The K loop is the 32x32 kernel's, run once per group into fresh INT32
+// accumulators; the scaled terms accumulate in FP32 registers next to them, so the
+// tiles are the smaller 32x32-kernel shapes (an FP32 copy of the 224-register
+// accumulators of the large kernels would not fit).
+template <class C>
+__global__ void __launch_bounds__(C::kThreads) grouped_summed_kernel(
+    const int8_t* __restrict__ a, const int8_t* __restrict__ w, const float* __restrict__ sa,
+    const uint16_t* __restrict__ sw, uint16_t* __restrict__ out, int groups, int m, int n,
+    int k, bool vec_n) {
+  // Every product and sum below is rounded on its own (no FMA contraction of the
+  // running sum with the scaled term), as the closed form requires.
+#pragma clang fp contract(off)
+  extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
+  auto* lds = (char __attribute__((address_space(3)))*)(lds_raw);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave_n = wave / C::WM;
+  const int wave_m = wave % C::WM;
+
+  const int tiles_n = (n + C::BN - 1) / C::BN;
+  const int tiles_m = (m + C::BM - 1) / C::BM;
+  const int blocks = tiles_n * tiles_m;
+  int logical = blockIdx.x;
+  {
+    const int per = blocks / kXcds, extra = blocks % kXcds;
+    const int xcd = logical % kXcds, idx = logical / kXcds;
+    logical = (xcd < extra ? xcd * (per + 1) : extra * (per + 1) + (xcd - extra) * per) + idx;
+  }
+  const int group_span = C::GROUP_M * tiles_n;
+  const int first_m = (logical / group_span) * C::GROUP_M;
+  const int group_rows = min(tiles_m - first_m, C::GROUP_M);
+  const int tile_m = first_m + (logical % group_span) % group_rows;
+  const int tile_n = (logical % group_span) / group_rows;
+  const int n0 = tile_n * C::BN, m0 = tile_m * C::BM;
+
+  // Lane holds D[n][m] for m = lane % 32 and n = 8*r4 + 4*(lane/32) + e.
+  const int frag_row = lane & 31;
+  const int frag_half = lane >> 5;
+  const int x_row0 = wave_n * (C::BN / C::WN);
+  const int y_row0 = wave_m * (C::BM / C::WM);
+
+  float chan_scale[C::TN][4][4];
+#pragma unroll
+  for (int i = 0; i < C::TN; ++i)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int col = n0 + x_row0 + i * 32 + r4 * 8 + frag_half * 4 + e;
+        chan_scale[i][r4][e] = col < n ? bf16_to_f32(sw[col]) : 0.f;
+      }
+
+  float sum[C::TN][C::TM][16];
+  for (int g = 0; g < groups; ++g) {
+    i32x16 acc[C::TN][C::TM];
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i)
+#pragma unroll
+      for (int j = 0; j < C::TM; ++j) acc[i][j] = i32x16{};
+    gemm_kloop<C, WeightCode::kSigned>(acc, a + int64_t(g) * m * k, w + int64_t(g) * n * k,
+                                       lds, wave, lane, wave_n, wave_m, m0, n0, m, n, k);
+    // Every wave is past its LDS reads before the next group's copies refill the ring.
+    __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+    __syncthreads();
+    float row_scale[C::TM];
+#pragma unroll
+    for (int j = 0; j < C::TM; ++j) {
+      const int row = m0 + y_row0 + j * 32 + frag_row;
+      row_scale[j] = row < m ? sa[int64_t(g) * m + row] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i)
+#pragma unroll
+      for (int j = 0; j < C::TM; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float term = (float(acc[i][j][v]) * row_scale[j]) * chan_scale[i][v >> 2][v & 3];
+          sum[i][j][v] = g == 0 ? term : sum[i][j][v] + term;
+        }
+  }
+
+#pragma unroll
+  for (int j = 0; j < C::TM; ++j) {
+    const int row = m0 + y_row0 + j * 32 + frag_row;
+    if (row >= m) continue;
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int col = n0 + x_row0 + i * 32 + r4 * 8 + frag_half * 4;
+        const int64_t base = int64_t(row) * n + col;
+        const float* v = &sum[i][j][r4 * 4];
+        if (vec_n) {
+          if (col < n)
+            *reinterpret_cast<u32x2*>(out + base) =
+                u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (col + e < n) out[base + e] = uint16_t(f32_to_bf16(v[e]));
+        }
+      }
+  }
+}
+
+template <class C>
+hipError_t run_grouped(const int8_t* a, const int8_t* w, const float* sa, const void* sw,
+                       void* out, int groups, int m, int n, int k, hipStream_t stream) {
+  auto kernel = grouped_summed_kernel<C>;
+  static bool configured = false;  // benign race: every thread sets the same attribute
+  if (!configured) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             C::kLdsBytes);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  const int blocks = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
+  const bool vec_n = n % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0;
+  kernel<<<blocks, C::kThreads, C::kLdsBytes, stream>>>(
+      a, w, sa, static_cast<const uint16_t*>(sw), static_cast<uint16_t*>(out), groups, m, n, k,
+      vec_n);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_channel_gemm(const int8_t* a, const void* w, WeightCode code,
@@ -1049,6 +1200,13 @@ hipError_t launch_channel_gemm(const int8_t* a, const void* w, WeightCode code,
                                                stream);
   return dispatch<WeightCode::kSigned, false>(a, w, sa, sw, out, nullptr, m, n, k, schedule,
                                               stream);
+}
+
+hipError_t launch_grouped_summed_gemm(const int8_t* a, const int8_t* w, const float* sa,
+                                      const void* sw, void* out, int groups, int m, int n,
+                                      int k, hipStream_t stream) {
+  if (m <= 32) return run_grouped<Small>(a, w, sa, sw, out, groups, m, n, k, stream);
+  return run_grouped<Medium>(a, w, sa, sw, out, groups, m, n, k, stream);
 }
 
 }  // namespace ci8

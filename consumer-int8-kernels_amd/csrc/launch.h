@@ -21,6 +21,12 @@ hipError_t launch_channel_gemm(const int8_t* a, const void* w, WeightCode code,
                                int32_t* workspace, int m, int n, int k, int schedule,
                                hipStream_t stream);
 
+// out = bf16(sum_g (float(A_g W_g^T) * sa[g]) * sw), A [groups, m, k], W [groups, n, k],
+// sa [groups, m]; FP32 sum over ascending g.
+hipError_t launch_grouped_summed_gemm(const int8_t* a, const int8_t* w, const float* sa,
+                                      const void* sw, void* out, int groups, int m, int n,
+                                      int k, hipStream_t stream);
+
 hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale, void* out,
                                int m, int n, int k, hipStream_t stream);
 

@@ -141,6 +141,30 @@ void channel_mm(Tensor a, Tensor w, Tensor sa, Tensor sw, Tensor out) {
                                 out.data_ptr(), m, n, k, stream_for(device)));
 }
 
+// No reference op: configs[4]'s grouped W8A8 with the group partials scaled and summed.
+void grouped_summed_mm(Tensor a, Tensor w, Tensor sa, Tensor sw, Tensor out) {
+  const int device = a.get_device_index();
+  check(a, ScalarType::Char, device);
+  check(w, ScalarType::Char, device);
+  check(sa, ScalarType::Float, device);
+  check(sw, ScalarType::BFloat16, device);
+  check(out, ScalarType::BFloat16, device);
+  STD_TORCH_CHECK(a.dim() == 3 && w.dim() == 3 && sa.dim() == 2 && sw.dim() == 1 &&
+                      out.dim() == 2,
+                  "Expected INT8 a[G,M,K], INT8 w[G,N,K], FP32 a_scale[G,M], BF16 "
+                  "w_scale[N], BF16 out[M,N]");
+  const int64_t g = a.size(0), m = a.size(1), k = a.size(2), n = w.size(1);
+  STD_TORCH_CHECK(w.size(0) == g && w.size(2) == k && sa.size(0) == g && sa.size(1) == m &&
+                      sw.size(0) == n && out.size(0) == m && out.size(1) == n,
+                  "Expected INT8 a[G,M,K], INT8 w[G,N,K], FP32 a_scale[G,M], BF16 "
+                  "w_scale[N], BF16 out[M,N]");
+  torch::stable::accelerator::DeviceGuard guard(device);
+  raise_on_error(ci8_grouped_summed_mm(static_cast<int8_t*>(a.data_ptr()),
+                                       static_cast<int8_t*>(w.data_ptr()),
+                                       static_cast<float*>(sa.data_ptr()), sw.data_ptr(),
+                                       out.data_ptr(), g, m, n, k, stream_for(device)));
+}
+
 // csrc/bindings.cpp:289-310
 void channel_gemv(Tensor x, Tensor w, Tensor scale, Tensor out) {
   const int device = x.get_device_index();
@@ -161,7 +185,7 @@ void channel_gemv(Tensor x, Tensor w, Tensor scale, Tensor out) {
 
 }  // namespace
 
-// Schemas: csrc/bindings.cpp:598, 603-606, 610.
+// Schemas: csrc/bindings.cpp:598, 603-606, 610; grouped_summed_mm has no reference op.
 STABLE_TORCH_LIBRARY(consumer_int8, m) {
   m.def("fused_channel_mm(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) out, int schedule=0) -> ()");
   m.def("quantize_rows(Tensor input, Tensor(a!) codes, Tensor(b!) scales) -> ()");
@@ -169,6 +193,7 @@ STABLE_TORCH_LIBRARY(consumer_int8, m) {
   m.def("channel_mm(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) out) -> ()");
   m.def("channel_gemv(Tensor x, Tensor w, Tensor scale, Tensor(a!) out) -> ()");
   m.def("cutlass_channel_mm(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) workspace, Tensor(b!) out) -> ()");
+  m.def("grouped_summed_mm(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) out) -> ()");
 }
 
 // HIP tensors carry the CUDA dispatch key in PyTorch-ROCm.
@@ -179,6 +204,7 @@ STABLE_TORCH_LIBRARY_IMPL(consumer_int8, CUDA, m) {
   m.impl("channel_mm", TORCH_BOX(&channel_mm));
   m.impl("channel_gemv", TORCH_BOX(&channel_gemv));
   m.impl("cutlass_channel_mm", TORCH_BOX(&cutlass_channel_mm));
+  m.impl("grouped_summed_mm", TORCH_BOX(&grouped_summed_mm));
 }
 
 extern "C" PyObject* PyInit__C() {

@@ -16,6 +16,8 @@
  *   ci8_fused_channel_mm     csrc/kernels.h:27-28, csrc/bindings.cpp:386-427, schema :598
  *   ci8_cutlass_channel_mm   csrc/kernels.h:63-65, csrc/bindings.cpp:386-424, schema :610
  *   ci8_channel_mm           csrc/kernels.h:56-58, csrc/bindings.cpp:238-265, schema :605
+ *   ci8_grouped_summed_mm    no reference op (configs[4]'s summed grouped W8A8); the
+ *                            closest reference code is benchmarks/cuda/q8_block_int8.cu:54-55
  *   ci8_channel_gemv         csrc/kernels.h:54-55, csrc/bindings.cpp:289-310, schema :606
  */
 #ifndef CONSUMER_INT8_AMD_H
@@ -92,6 +94,21 @@ int ci8_cutlass_channel_mm(const int8_t* a, const int8_t* w, const float* a_scal
 int ci8_channel_mm(const int8_t* a, const uint8_t* w_u8, const float* a_scale,
                    const void* w_scale, void* out, int64_t m, int64_t n, int64_t k,
                    void* stream);
+
+/* grouped_summed_mm: grouped W8A8 with the per-group partials scaled and summed,
+ *   out BF16 [m,n] = bf16_rn( t_0 + t_1 + ... + t_{groups-1} )  (FP32 adds, ascending g),
+ *   t_g = fl( fl( float_rn(a[g] . w[g]^T) * a_scale[g,m] ) * float(w_scale[n]) ),
+ * with a INT8 [groups,m,k] (the codes quantize_grouped4096 writes for k = 4096),
+ * w INT8 [groups,n,k], a_scale FP32 [groups,m], w_scale BF16 [n].
+ * Requires groups > 0, m,n,k > 0, k % 32 == 0, k <= 65536, n % 4 == 0, each group's a,
+ * w and out <= INT_MAX elements, a and w 16-byte aligned.
+ * No reference counterpart: the reference has per-group fused_channel_mm calls with
+ * separate outputs (benchmarks/benchmark_grouped_w8a8.py:100-107) and an FP32 sum of
+ * scaled INT32 block partials (benchmarks/cuda/q8_block_int8.cu:54-55); this entry point
+ * is the build's closed form for configs[4]. */
+int ci8_grouped_summed_mm(const int8_t* a, const int8_t* w, const float* a_scale,
+                          const void* w_scale, void* out, int64_t groups, int64_t m,
+                          int64_t n, int64_t k, void* stream);
 
 /* channel_gemv (W8A16): out BF16 [m,n] = bf16_rn(sum_k float(x[m,k]) * wq[n,k]) with
  * wq[n,k] = bf16_rn(float(w[n,k]) * float(scale[n])) and FP32 accumulation; x BF16

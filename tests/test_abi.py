@@ -21,7 +21,7 @@ def test_header_declares_the_expected_entry_points():
     assert declared_functions() == sorted([
         "ci8_last_error", "ci8_version", "ci8_quantize_rows", "ci8_quantize_grouped4096",
         "ci8_fused_channel_mm", "ci8_cutlass_channel_mm", "ci8_channel_mm",
-        "ci8_channel_gemv",
+        "ci8_channel_gemv", "ci8_grouped_summed_mm",
     ])
 
 
@@ -114,6 +114,20 @@ def test_channel_mm_and_gemv_rejections(lib):
            A.CI8_ERR_ALIGNMENT, "Unaligned vector inputs")
 
 
+def test_grouped_summed_rejections(lib):
+    from consumer_int8 import _abi as A
+
+    msg = "Invalid grouped GEMM geometry"
+    for g, m, n, k in [(0, 4, 4, 32), (2, 0, 4, 32), (2, 4, 6, 32), (2, 4, 4, 48),
+                       (2, 4, 4, 65568)]:
+        expect(lib, lib.ci8_grouped_summed_mm(FAKE, FAKE, FAKE, FAKE, FAKE, g, m, n, k, None),
+               A.CI8_ERR_GEOMETRY, msg)
+    expect(lib, lib.ci8_grouped_summed_mm(FAKE + 8, FAKE, FAKE, FAKE, FAKE, 2, 4, 4, 32, None),
+           A.CI8_ERR_ALIGNMENT, "grouped_summed_mm requires aligned buffers")
+    expect(lib, lib.ci8_grouped_summed_mm(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 1 << 16, 4, 1 << 16,
+                                          None), A.CI8_ERR_TOO_LARGE, "Matrix too large")
+
+
 def test_torch_surface_matches_reference_schemas():
     import torch
 
@@ -126,6 +140,8 @@ def test_torch_surface_matches_reference_schemas():
         "channel_mm": "(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) out) -> ()",
         "channel_gemv": "(Tensor x, Tensor w, Tensor scale, Tensor(a!) out) -> ()",
         "cutlass_channel_mm": "(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) workspace, Tensor(b!) out) -> ()",
+        # no reference counterpart (configs[4]'s summed grouped W8A8)
+        "grouped_summed_mm": "(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) out) -> ()",
     }
     for name, schema in expected.items():
         handle = getattr(ops, name)
