@@ -9,9 +9,11 @@ GEMM. Inputs are resident in HBM before timing; the weights, activations and cod
 rotate over enough copies that no step finds its inputs in the 256 MB Infinity Cache.
 
 Also reported: `roofline` for the dominant kernel (the GEMM, timed per launch with HIP
-events on the stream it runs on), the quantizer and the W8A16 GEMV as
-extra roofline lines, and `cpu_baseline`, the CPU oracle on a bounded row slice of the
-same workload on this host's cores.
+events on the stream it runs on); extra roofline lines for the quantizer, the W8A16
+GEMV, the grouped summed GEMM, the biased-UINT8 down
+projection and the small quantize + GEMM pass; and
+`cpu_baseline`, the CPU oracle on a bounded row slice of the same workload on this
+host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-extras]
                       [--copy-calibration]
@@ -251,6 +253,71 @@ def main() -> int:
                                             "peak": PEAK_HBM_GBS, "unit": "GB/s",
                                             "frac": round(gbs / PEAK_HBM_GBS, 4),
                                             "mean_us": round(mean_us, 2), "bytes": gemv_bytes(m)}
+        del gw, gs
+        # grouped W8A8 summed over 4 groups of 4096, M=2048, N=4096 (4 weight
+        # copies of 67 MB rotate, more than the MALL holds together with the codes).
+        G5, M5, N5, K5 = 4, 2048, 4096, 4096
+        c5 = torch.randint(-127, 128, (G5, M5, K5), generator=gen, device="cuda", dtype=torch.int8)
+        s5 = torch.rand(G5, M5, generator=gen, device="cuda") / 127
+        w5 = [torch.randint(-127, 128, (G5, N5, K5), generator=gen, device="cuda",
+                            dtype=torch.int8) for _ in range(4)]
+        sw5 = (torch.rand(N5, generator=gen, device="cuda") * 9e-3 + 1e-3).to(torch.bfloat16)
+        o5 = torch.empty(M5, N5, device="cuda", dtype=torch.bfloat16)
+        calls = [lambda i=i: ops.grouped_summed_mm(c5, w5[i], s5, sw5, o5) for i in range(4)]
+        for c in calls:
+            c()
+        mean_us, _ = time_kernel(torch, calls, 20)
+        tops = 2 * M5 * N5 * G5 * K5 / (mean_us * 1e-6) / 1e12
+        extras["grouped_summed_mm_cfg5"] = {"bound": "mfma", "achieved": round(tops, 1),
+                                            "peak": round(peak_tops, 1), "unit": "TFLOP/s",
+                                            "frac": round(tops / peak_tops, 4),
+                                            "mean_us": round(mean_us, 2),
+                                            "ops": 2 * M5 * N5 * G5 * K5}
+        del c5, s5, w5, o5
+        # down projection M=16384, K=17408, N=5120 with biased UINT8 weights.
+        M4, K4, N4 = 16384, 17408, 5120
+        a4 = torch.randint(-127, 128, (M4, K4), generator=gen, device="cuda", dtype=torch.int8)
+        s4 = torch.rand(M4, generator=gen, device="cuda") / 127
+        w4 = [torch.randint(0, 256, (N4, K4), generator=gen, device="cuda", dtype=torch.uint8)
+              for _ in range(2)]
+        sw4 = (torch.rand(N4, generator=gen, device="cuda") * 9e-3 + 1e-3).to(torch.bfloat16)
+        o4 = torch.empty(M4, N4, device="cuda", dtype=torch.bfloat16)
+        calls = [lambda i=i: ops.channel_mm(a4, w4[i], s4, sw4, o4) for i in range(2)]
+        for c in calls:
+            c()
+        mean_us, _ = time_kernel(torch, calls, 6)
+        tops = 2 * M4 * N4 * K4 / (mean_us * 1e-6) / 1e12
+        extras["channel_mm_cfg4"] = {"bound": "mfma", "achieved": round(tops, 1),
+                                     "peak": round(peak_tops, 1), "unit": "TFLOP/s",
+                                     "frac": round(tops / peak_tops, 4),
+                                     "mean_us": round(mean_us, 2), "ops": 2 * M4 * N4 * K4}
+        del a4, s4, w4, o4
+        # quantize_rows + fused_channel_mm at M=128, K=4096, N=4096; AI 234
+        # op/B is below the ridge, so this small case is bounded by HBM (bytes below).
+        M1, K1, N1 = 128, 4096, 4096
+        x1 = torch.randn(M1, K1, generator=gen, device="cuda").to(torch.bfloat16)
+        c1 = torch.empty(M1, K1, device="cuda", dtype=torch.int8)
+        s1 = torch.empty(M1, device="cuda")
+        w1 = [torch.randint(-127, 128, (N1, K1), generator=gen, device="cuda", dtype=torch.int8)
+              for _ in range(16)]
+        sw1 = (torch.rand(N1, generator=gen, device="cuda") * 9e-3 + 1e-3).to(torch.bfloat16)
+        o1 = torch.empty(M1, N1, device="cuda", dtype=torch.bfloat16)
+
+        def cfg1(i):
+            ops.quantize_rows(x1, c1, s1)
+            ops.fused_channel_mm(c1, w1[i], s1, sw1, o1, 0)
+
+        calls = [lambda i=i: cfg1(i) for i in range(16)]
+        for c in calls:
+            c()
+        mean_us, _ = time_kernel(torch, calls, 48)
+        b1 = 3 * M1 * K1 + 4 * M1 + N1 * K1 + 2 * N1 + 2 * M1 * N1 + M1 * K1 + 4 * M1
+        extras["quantize_fused_cfg1"] = {"bound": "hbm", "achieved": round(b1 / (mean_us * 1e-6) / 1e9, 1),
+                                         "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                         "frac": round(b1 / (mean_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                                         "mean_us": round(mean_us, 2), "bytes": b1,
+                                         "tops": round(2 * M1 * N1 * K1 / (mean_us * 1e-6) / 1e12, 1)}
+        del x1, c1, s1, w1, o1
         result["extras"] = extras
 
     if args.copy_calibration:
