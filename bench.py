@@ -83,19 +83,21 @@ def make_inputs(torch, gen, copies_w=3, copies_x=3):
     return xs, ws, sw, codes, sa, out
 
 
-def time_kernel(torch, calls, reps):
-    """Mean and median per-launch time (us) of a rotating list of launch closures,
-    each bracketed by HIP events on the current stream."""
+def time_kernel(torch, calls, reps, batch=10):
+    """Mean and median per-launch time (us) of a rotating list of launch closures:
+    `reps` event pairs on the current stream, each around `batch` back-to-back launches
+    (so the per-launch figure carries no event or launch-gap overhead of its own)."""
     events = []
-    for i in range(reps):
+    for r in range(reps):
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         start.record()
-        calls[i % len(calls)]()
+        for i in range(batch):
+            calls[(r * batch + i) % len(calls)]()
         end.record()
         events.append((start, end))
     torch.cuda.synchronize()
-    times = [s.elapsed_time(e) * 1e3 for s, e in events]
+    times = [s.elapsed_time(e) * 1e3 / batch for s, e in events]
     return statistics.mean(times), statistics.median(times)
 
 
@@ -231,7 +233,7 @@ def main() -> int:
         calls = [lambda i=i: ops.quantize_rows(qx[i], qc[i], sa) for i in range(5)]
         for c in calls:
             c()
-        mean_us, med_us = time_kernel(torch, calls, 50)
+        mean_us, med_us = time_kernel(torch, calls, 10)
         gbs = QUANT_BYTES / (mean_us * 1e-6) / 1e9
         extras["quantize_rows"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                                    "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
@@ -247,7 +249,7 @@ def main() -> int:
             calls = [lambda i=i: ops.channel_gemv(gx, gw[i], gs, go) for i in range(4)]
             for c in calls:
                 c()
-            mean_us, med_us = time_kernel(torch, calls, 40)
+            mean_us, med_us = time_kernel(torch, calls, 8)
             gbs = gemv_bytes(m) / (mean_us * 1e-6) / 1e9
             extras[f"channel_gemv_m{m}"] = {"bound": "hbm", "achieved": round(gbs, 1),
                                             "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -266,7 +268,7 @@ def main() -> int:
         calls = [lambda i=i: ops.grouped_summed_mm(c5, w5[i], s5, sw5, o5) for i in range(4)]
         for c in calls:
             c()
-        mean_us, _ = time_kernel(torch, calls, 20)
+        mean_us, _ = time_kernel(torch, calls, 4)
         tops = 2 * M5 * N5 * G5 * K5 / (mean_us * 1e-6) / 1e12
         extras["grouped_summed_mm_cfg5"] = {"bound": "mfma", "achieved": round(tops, 1),
                                             "peak": round(peak_tops, 1), "unit": "TFLOP/s",
@@ -285,7 +287,7 @@ def main() -> int:
         calls = [lambda i=i: ops.channel_mm(a4, w4[i], s4, sw4, o4) for i in range(2)]
         for c in calls:
             c()
-        mean_us, _ = time_kernel(torch, calls, 6)
+        mean_us, _ = time_kernel(torch, calls, 2, batch=4)
         tops = 2 * M4 * N4 * K4 / (mean_us * 1e-6) / 1e12
         extras["channel_mm_cfg4"] = {"bound": "mfma", "achieved": round(tops, 1),
                                      "peak": round(peak_tops, 1), "unit": "TFLOP/s",
@@ -310,7 +312,7 @@ def main() -> int:
         calls = [lambda i=i: cfg1(i) for i in range(16)]
         for c in calls:
             c()
-        mean_us, _ = time_kernel(torch, calls, 48)
+        mean_us, _ = time_kernel(torch, calls, 8)
         b1 = 3 * M1 * K1 + 4 * M1 + N1 * K1 + 2 * N1 + 2 * M1 * N1 + M1 * K1 + 4 * M1
         extras["quantize_fused_cfg1"] = {"bound": "hbm", "achieved": round(b1 / (mean_us * 1e-6) / 1e9, 1),
                                          "peak": PEAK_HBM_GBS, "unit": "GB/s",

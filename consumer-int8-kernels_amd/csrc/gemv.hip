@@ -26,6 +26,9 @@
 //  * One barrier per stage. The ring has three slots, held in three separate LDS
 //    arrays so the compiler can see that the slot being read is not the slot an
 //    in-flight copy is writing.
+// For small batches (m <= 4, x small enough to sit in LDS) a second kernel copies all
+// of x into LDS once and then lets every wave stream its W with three stages of loads
+// in flight and no barriers at all, which removes the per-stage lock-step of the ring.
 // Weight rows past N and K chunks past K read as zero through the buffer range check.
 #include "ci8_device.h"
 #include "launch.h"
@@ -229,12 +232,163 @@ __global__ void __launch_bounds__(C::kThreads) channel_gemv_kernel(
   }
 }
 
+
+// ---------------------------------------------------------------------------------
+// Small-batch variant: x resident in LDS. The LDS holds x[0:m, :] as rows of kblocks
+// 128-byte blocks (16-byte chunks XOR-swizzled by row & 7) followed by 1 KiB of zeros;
+// lanes for batch rows >= m, and K blocks past a wave's range, read the zeros. Wave
+// (cb, range) streams 16 channels x its K range of W, kAhead stages of kU blocks ahead.
+template <int kCB_, int kS_, int kU_, int kAhead_>
+struct ResidentConfig {
+  static constexpr int kCB = kCB_, kS = kS_, kU = kU_, kAhead = kAhead_;
+  static constexpr int kWaves = kCB * kS;
+  static constexpr int kThreads = 64 * kWaves;
+};
+
+inline int resident_lds_bytes(int m, int k) { return m * ((k + 63) / 64) * 128 + 1024; }
+
+template <class C, int R>
+__device__ __forceinline__ void resident_stage(int t, __amdgpu_buffer_rsrc_t w_rsrc,
+                                               uint32_t w_base, int lane_col, int kb_first,
+                                               int kend, int k, u32x4 (&wv)[C::kAhead][C::kU],
+                                               f32x4& acc, const lds_char* xs,
+                                               bool row_live, uint32_t x_row, uint32_t x_zero,
+                                               int group, int row, float s, float bias) {
+  waitcnt<vmcnt_imm((C::kAhead - 1) * C::kU)>();  // W(t) landed, later stages in flight
+#pragma unroll
+  for (int j = 0; j < C::kU; ++j) {
+    const int kb = kb_first + t * C::kU + j;  // wave-uniform
+    // Batch rows >= m and blocks past this wave's range read the zero KiB.
+    const uint32_t base = row_live && kb < kend ? x_row + uint32_t(kb * 128) : x_zero;
+    u32x4 xf[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      xf[h] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+          xs + base + (((2 * group + h) ^ (row & 7)) * 16));
+    const u32x4 wq = wv[R][j];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t w0 = wq[2 * h] ^ 0x80808080u;
+      const uint32_t w1 = wq[2 * h + 1] ^ 0x80808080u;
+      acc = mfma_bf16(u32x4{dequant_pair(w0, 0, s, bias), dequant_pair(w0, 16, s, bias),
+                            dequant_pair(w1, 0, s, bias), dequant_pair(w1, 16, s, bias)},
+                      xf[h], acc);
+    }
+  }
+  // Refill this register slot with stage t + kAhead.
+#pragma unroll
+  for (int j = 0; j < C::kU; ++j) {
+    const int kb = kb_first + (t + C::kAhead) * C::kU + j;
+    const bool valid = kb < kend && kb * 64 + lane_col < k;
+    wv[R][j] = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                   w_rsrc, valid ? w_base + uint32_t(kb * 64) : kOutOfRange, 0, 0));
+  }
+}
+
+template <class C>
+__global__ void __launch_bounds__(C::kThreads) channel_gemv_resident_kernel(
+    const uint16_t* __restrict__ x, const int8_t* __restrict__ w,
+    const uint16_t* __restrict__ scale, uint16_t* __restrict__ out, int m, int n, int k) {
+  static_assert(C::kAhead == 3, "the stage loop below is unrolled for three slots");
+  extern __shared__ __attribute__((aligned(1024))) char xs_raw[];
+  __shared__ f32x4 partial[C::kWaves][64];
+  const lds_char* xs = (const lds_char*)xs_raw;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int cb = wave % C::kCB, range = wave / C::kCB;
+  const int row = lane & 15, group = lane >> 4;
+  const int channel = blockIdx.x * 16 * C::kCB + cb * 16 + row;
+
+  const auto w_rsrc = make_rsrc(w, uint32_t(n) * uint32_t(k));
+  const auto x_rsrc = make_rsrc(x, uint32_t(m) * uint32_t(k) * 2u);
+  const float s = channel < n ? bf16_to_f32(scale[channel]) : 0.f;
+  const float bias = -128.f * s;
+  const uint32_t w_base =
+      channel < n ? uint32_t(channel) * uint32_t(k) + uint32_t(group * 16) : kOutOfRange;
+  const int kblocks = (k + 63) / 64;
+  const int range_len = (kblocks + C::kS - 1) / C::kS;
+  const int kb_first = range * range_len;
+  const int kend = min(kb_first + range_len, kblocks);
+  const int stages = (range_len + C::kU - 1) / C::kU;
+
+  // W first (the long-latency stream): stages 0 .. kAhead-1.
+  u32x4 wv[C::kAhead][C::kU];
+#pragma unroll
+  for (int a = 0; a < C::kAhead; ++a)
+#pragma unroll
+    for (int j = 0; j < C::kU; ++j) {
+      const int kb = kb_first + a * C::kU + j;
+      const bool valid = kb < kend && kb * 64 + group * 16 < k;
+      wv[a][j] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     w_rsrc, valid ? w_base + uint32_t(kb * 64) : kOutOfRange, 0, 0));
+    }
+
+  // Copy x: 16-byte unit u of LDS row r holds global chunk (u % 8) ^ (r & 7) of block
+  // u / 8. The last copy may spill past the rows into the zero KiB, writing zeros.
+  const int row_units = kblocks * 8;
+  const int units = m * row_units;
+  const uint32_t zero_off = uint32_t(units) * 16u;
+  for (int u0 = wave * 64; u0 < units; u0 += C::kWaves * 64) {
+    const int u = u0 + lane;
+    const int r = u / row_units, within = u % row_units;
+    const int kb = within >> 3, c = (within & 7) ^ (r & 7);
+    const bool valid = u < units && kb * 64 + c * 8 < k;
+    copy16(x_rsrc, reinterpret_cast<lds_void*>((lds_char*)xs_raw + u0 * 16),
+           valid ? uint32_t(r) * uint32_t(k) * 2u + uint32_t(kb * 128 + c * 16) : kOutOfRange);
+  }
+  for (int i = threadIdx.x; i < 64; i += C::kThreads)
+    reinterpret_cast<u32x4*>(xs_raw + zero_off)[i] = u32x4{0, 0, 0, 0};
+  waitcnt<vmcnt_imm(0)>();
+  __syncthreads();
+
+  const bool row_live = row < m;
+  const uint32_t x_row = uint32_t(row * kblocks * 128);
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < stages; t += 3) {
+    resident_stage<C, 0>(t, w_rsrc, w_base, group * 16, kb_first, kend, k, wv, acc, xs,
+                         row_live, x_row, zero_off, group, row, s, bias);
+    if (t + 1 >= stages) break;
+    resident_stage<C, 1>(t + 1, w_rsrc, w_base, group * 16, kb_first, kend, k, wv, acc, xs,
+                         row_live, x_row, zero_off, group, row, s, bias);
+    if (t + 2 >= stages) break;
+    resident_stage<C, 2>(t + 2, w_rsrc, w_base, group * 16, kb_first, kend, k, wv, acc, xs,
+                         row_live, x_row, zero_off, group, row, s, bias);
+  }
+  waitcnt<vmcnt_imm(0)>();  // drain the trailing (out-of-range) loads before exit
+
+  partial[wave][lane] = acc;
+  __syncthreads();
+  for (int slot = threadIdx.x; slot < C::kCB * 64 * 4; slot += C::kThreads) {
+    const int e = slot & 3, l = (slot >> 2) & 63, b = slot >> 8;
+    const int out_row = l & 15;
+    const int out_col = blockIdx.x * 16 * C::kCB + b * 16 + (l >> 4) * 4 + e;
+    if (out_row >= m || out_col >= n) continue;
+    float sum = partial[b][l][e];
+#pragma unroll
+    for (int v = 1; v < C::kS; ++v) sum += partial[v * C::kCB + b][l][e];
+    out[int64_t(out_row) * n + out_col] = uint16_t(f32_to_bf16(sum));
+  }
+}
+
 }  // namespace
 
 hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale, void* out,
                                int m, int n, int k, hipStream_t stream) {
-  // Measured on MI355X at K=5120, N=17408: 2 channel blocks x 2 K ranges with 4-block
-  // stages beat 1/4 channel blocks, 1/4 ranges and 8-block stages at every m <= 16.
+  // Measured on MI355X at K=5120, N=17408: x resident in LDS with 1 channel block x 4 K
+  // ranges wins for m <= 4; above that the LDS copy limits occupancy and the ring with
+  // 2 channel blocks x 2 K ranges and 4-block stages is faster.
+  const int lds = resident_lds_bytes(m, k);
+  if (m <= 4 && lds <= 60 * 1024) {  // plus 4 KiB of static LDS: within the 64 KiB default
+    using R = ResidentConfig<1, 4, 4, 3>;
+    const int grid = (n + 16 * R::kCB - 1) / (16 * R::kCB);
+    channel_gemv_resident_kernel<R><<<grid, R::kThreads, lds, stream>>>(
+        static_cast<const uint16_t*>(x), w, static_cast<const uint16_t*>(scale),
+        static_cast<uint16_t*>(out), m, n, k);
+    return hipGetLastError();
+  }
   using C = GemvConfig<2, 2, 4>;
   const int grid = (n + 16 * C::kCB - 1) / (16 * C::kCB);
   channel_gemv_kernel<C><<<grid, C::kThreads, 0, stream>>>(
