@@ -742,8 +742,12 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_k128_kernel(
 // no sharing, no extra traffic), while the 224 W rows, used by all four waves, go
 // through an LDS ring filled by buffer_load ... lds. With only W in LDS a stage of 128
 // K-bytes is 28 KB, so a ring of four slots keeps three stages in flight, and the A
-// loads of the next stage are in flight in a second register set: about 116 KB of
-// operands in flight per CU (twice what fits when both operands share LDS).
+// loads of the next two stages are in flight in two more register sets (three sets in
+// all): about 124 KB of operands in flight per CU (twice what fits when both operands
+// share LDS). Measured with per-wave clocks on MI355X, the main loop is limited by the
+// vector-memory path (TA/L1) feeding the A loads, whose 16-row x 64-byte pattern moves
+// fewer bytes per cycle than whole-line copies; loading A two stages ahead instead of
+// one saves about 4% of the cycles per stage.
 //
 // K order: within a 128-byte stage, MFMA lane group g (lane / 16) takes physical chunk
 // 2g + h in K-step h (0 or 1). A and W use the same order, so the dot products are
@@ -751,7 +755,7 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_k128_kernel(
 // of its row.
 //
 // For stage t (K-steps h = 0, 1), each wave:
-//   h = 0: issue the A loads of stage t+1 (into the other register set); 56 MFMAs;
+//   h = 0: issue the A loads of stage t+2 (into the set stage t-1 used); 56 MFMAs;
 //          reload each W fragment for K-step (t, 1) right after its last MFMA;
 //   sync:  own W copies of stage t+1 landed, then a barrier (all waves' copies landed;
 //          every wave finished K-step (t, 0), so nobody reads the slot of stage t-1);
@@ -856,7 +860,7 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
       a_voff[j][h] = row < m ? uint32_t(row) * uint32_t(k) + uint32_t(frag_group * 32 + h * 16)
                              : kOutOfRange;
   }
-  i32x4 af[2][2][C::TM];  // [register set][K-step][m block]
+  i32x4 af[3][2][C::TM];  // [register set][K-step][m block]
   auto load_a = [&] __device__(int t, int set) __attribute__((always_inline)) {
     const int st = t < ns ? t : 0;
     const int k0 = st * C::BK;
@@ -922,17 +926,18 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
     }
   };
   // Before K-step (t, 1): own W copies of stage t+1 landed. Vector-memory operations
-  // are counted in issue order; after those copies this wave issued the copies of
-  // stages t+2 .. t+kAhead-1 and the A loads of stages t (steady state only; already
-  // consumed by K-step (t, 0)) and t+1, so allowing the last two groups outstanding
-  // guarantees stage t+1 (and is exact for t = 0, where the prologue issued W copies
-  // 0..kAhead-1 before A stage 1).
+  // are counted in issue order: ..., A(t+1), W(t+2), A(t+2), so with the W copies of
+  // stage t+1 issued before A(t+1) (stage t-1 issues A(t+1) then W(t+2); the prologue
+  // issues W0 A0 W1 A1 W2 so t = 0 follows the same pattern), allowing A(t+1), W(t+2)
+  // and A(t+2) outstanding guarantees W(t+1).
   auto sync = [&] __device__() __attribute__((always_inline)) {
-    waitcnt<vmcnt_imm((C::kAhead - 2) * C::kLoads + 2 * C::TM)>();
+    waitcnt<vmcnt_imm((C::kAhead - 2) * C::kLoads + 4 * C::TM)>();
     workgroup_barrier();
   };
+  // A is loaded two stages ahead into three register sets (set = stage % 3): the loads
+  // of stage t+2 go into the set stage t-1 used.
   auto stage = [&] __device__(int t, int set) __attribute__((always_inline)) {
-    load_a(t + 1, set ^ 1);
+    load_a(t + 2, (set + 2) % 3);
     kstep(set, 0, t, 1);
     sched_kstep(std::integral_constant<int, 0x020>{}, std::integral_constant<int, 2 * C::TM>{});
     sync();
@@ -941,25 +946,29 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
     sched_kstep(std::integral_constant<int, 0x010>{}, std::integral_constant<int, C::kLoads>{});
   };
 
-  // Prologue: W stages 0..kAhead-1 and A stage 0; the W fragments of K-step (0, 0).
-  // Issue order matters: the compiler's vector-memory counter tracking at the loop head
-  // merges this prologue's state, so A stage 0 must precede the later W copies.
+  // Prologue: W0 A0 W1 A1 W2 (the steady-state order), then the W fragments of K-step
+  // (0, 0). The scheduling barriers keep that order.
+  static_assert(C::kAhead == 3, "prologue issues W stages 0..2");
   issue_w(0);
   load_a(0, 0);
   __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int t = 1; t < C::kAhead; ++t) issue_w(t);
-  waitcnt<vmcnt_imm((C::kAhead - 1) * C::kLoads)>();  // W stage 0 and A stage 0 landed
+  issue_w(1);
+  load_a(1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  issue_w(2);
+  waitcnt<vmcnt_imm(2 * C::kLoads + 2 * C::TM)>();  // W(0) and A(0) landed
   workgroup_barrier();
 #pragma unroll
   for (int i = 0; i < C::TN; ++i) xf[i] = ld(xaddr(0, 0, i));
 
   int t = 0;
-  for (; t + 1 < ns; t += 2) {
+  for (; t + 2 < ns; t += 3) {
     stage(t, 0);
     stage(t + 1, 1);
+    stage(t + 2, 2);
   }
   if (t < ns) stage(t, 0);
+  if (t + 1 < ns) stage(t + 1, 1);
   waitcnt<vmcnt_imm(0)>();  // copies past the last stage
 
   store_tile16<C::TM, C::TN, kWorkspace>(acc, m0 + wave * (C::BM / C::kWaves), n0, m, n, sa, sw,
