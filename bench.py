@@ -11,7 +11,8 @@ rotate over enough copies that no step finds its inputs in the 256 MB Infinity C
 Also reported: `roofline` for the dominant kernel (the GEMM, timed per launch with HIP
 events on the stream it runs on); extra roofline lines for the quantizer, the W8A16
 GEMV, the grouped summed GEMM, the biased-UINT8 down
-projection and the small quantize + GEMM pass; and
+projection and its SwiGLU activation producers (silu_mul_quantize,
+silu_mul), and the small quantize + GEMM pass; and
 `cpu_baseline`, the CPU oracle on a bounded row slice of the same workload on this
 host's cores.
 
@@ -294,6 +295,28 @@ def main() -> int:
                                      "frac": round(tops / peak_tops, 4),
                                      "mean_us": round(mean_us, 2), "ops": 2 * M4 * N4 * K4}
         del a4, s4, w4, o4
+        # configs[3]'s activation producer: SwiGLU of BF16 [16384, 2*17408] quantized per
+        # row (silu_mul_quantize), and the unquantized silu_mul, both far beyond the MALL.
+        xs = torch.randn(M4, 2 * K4, generator=gen, device="cuda").to(torch.bfloat16)
+        cs = torch.empty(M4, K4, device="cuda", dtype=torch.int8)
+        ss = torch.empty(M4, device="cuda")
+        ops.silu_mul_quantize(xs, cs, ss)
+        mean_us, _ = time_kernel(torch, [lambda: ops.silu_mul_quantize(xs, cs, ss)], 3, batch=4)
+        bs = 4 * M4 * K4 + M4 * K4 + 4 * M4
+        extras["silu_mul_quantize_cfg4"] = {"bound": "hbm", "achieved": round(bs / (mean_us * 1e-6) / 1e9, 1),
+                                            "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                            "frac": round(bs / (mean_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                                            "mean_us": round(mean_us, 2), "bytes": bs}
+        del cs, ss
+        act = torch.empty(M4, K4, device="cuda", dtype=torch.bfloat16)
+        ops.silu_mul(xs, act)
+        mean_us, _ = time_kernel(torch, [lambda: ops.silu_mul(xs, act)], 3, batch=4)
+        bs = 4 * M4 * K4 + 2 * M4 * K4
+        extras["silu_mul_cfg4"] = {"bound": "hbm", "achieved": round(bs / (mean_us * 1e-6) / 1e9, 1),
+                                   "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                   "frac": round(bs / (mean_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                                   "mean_us": round(mean_us, 2), "bytes": bs}
+        del xs, act
         # quantize_rows + fused_channel_mm at M=128, K=4096, N=4096; AI 234
         # op/B is below the ridge, so this small case is bounded by HBM (bytes below).
         M1, K1, N1 = 128, 4096, 4096

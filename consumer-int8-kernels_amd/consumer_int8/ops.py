@@ -1,7 +1,7 @@
 """Ahead-of-time operators. Buffers belong to the caller; importing never compiles code.
 
 Same handles and schemas as the reference's operator surface
-(src/consumer_int8/ops.py:20-32; schemas csrc/bindings.cpp:598-610), implemented by
+(src/consumer_int8/ops.py:18-32; schemas csrc/bindings.cpp:594-610), implemented by
 hand-written gfx950 kernels in libci8_amd.so and registered for the CUDA dispatch key
 (the key PyTorch-ROCm uses for HIP tensors) by the _C module.
 
@@ -26,6 +26,12 @@ grouped_summed_mm(a, w, a_scale, w_scale, out)
     (quantize_grouped4096's codes), w INT8 [G,N,K], a_scale FP32 [G,M], w_scale BF16 [N];
     out = bf16(sum over ascending g of (float(a[g] @ w[g].T) * a_scale[g, :, None])
     * w_scale[None, :]), each term rounded to FP32 and summed in FP32.
+silu_mul(input, out)
+    SwiGLU: input BF16 [M,2K] = [gate | up], K in {8704, 17408}; out BF16 [M,K] =
+    bf16(silu(gate) * up) computed in FP32 (silu(g) = g / (1 + exp(-g))).
+silu_mul_quantize(input, codes, scales)
+    The silu_mul activations quantized per row exactly as quantize_rows, without
+    writing them out: codes INT8 [M,K], scales FP32 [M].
 """
 
 import torch
@@ -39,6 +45,8 @@ channel_gemv = torch.ops.consumer_int8.channel_gemv
 cutlass_channel_mm = torch.ops.consumer_int8.cutlass_channel_mm
 fused_channel_mm = torch.ops.consumer_int8.fused_channel_mm
 grouped_summed_mm = torch.ops.consumer_int8.grouped_summed_mm
+silu_mul = torch.ops.consumer_int8.silu_mul
+silu_mul_quantize = torch.ops.consumer_int8.silu_mul_quantize
 
 
 @torch.library.register_fake("consumer_int8::fused_channel_mm")
@@ -73,4 +81,14 @@ def _cutlass_channel_mm_fake(a, w, a_scale, w_scale, workspace, out):
 
 @torch.library.register_fake("consumer_int8::grouped_summed_mm")
 def _grouped_summed_mm_fake(a, w, a_scale, w_scale, out):
+    return None
+
+
+@torch.library.register_fake("consumer_int8::silu_mul")
+def _silu_mul_fake(input, out):
+    return None
+
+
+@torch.library.register_fake("consumer_int8::silu_mul_quantize")
+def _silu_mul_quantize_fake(input, codes, scales):
     return None

@@ -156,4 +156,29 @@ int ci8_channel_gemv(const void* x, const int8_t* w, const void* scale, void* ou
       ci8::launch_channel_gemv(x, w, scale, out, int(m), int(n), int(k), as_stream(stream)));
 }
 
+// csrc/bindings.cpp:36-40: the two SwiGLU widths of the reference's models.
+int ci8_silu_mul(const void* x, void* out, int64_t m, int64_t k, void* stream) {
+  if (!(m >= 0 && (k == 8704 || k == 17408) && m * 2 * k <= INT_MAX))
+    return fail(CI8_ERR_GEOMETRY, "Unsupported SwiGLU shape");
+  if (!aligned(x, 2) || !aligned(out, 2))
+    return fail(CI8_ERR_ALIGNMENT, "SwiGLU requires aligned buffers");
+  if (overlap(x, m * 2 * k * 2, out, m * k * 2))
+    return fail(CI8_ERR_OVERLAP, "SwiGLU buffers must not overlap");
+  return launched(ci8::launch_silu_mul(x, out, int(m), int(k), as_stream(stream)));
+}
+
+// csrc/bindings.cpp:51-59
+int ci8_silu_mul_quantize(const void* x, int8_t* codes, float* scales, int64_t m, int64_t k,
+                          void* stream) {
+  if (!(m >= 0 && (k == 8704 || k == 17408) && m * 2 * k <= INT_MAX))
+    return fail(CI8_ERR_GEOMETRY, "Unsupported SwiGLU quantization shape");
+  if (!aligned(x, 16) || !aligned(codes, 8) || !aligned(scales, 4))
+    return fail(CI8_ERR_ALIGNMENT, "SwiGLU quantization requires aligned buffers");
+  if (overlap(x, m * 2 * k * 2, codes, m * k) || overlap(x, m * 2 * k * 2, scales, m * 4) ||
+      overlap(codes, m * k, scales, m * 4))
+    return fail(CI8_ERR_OVERLAP, "SwiGLU quantization buffers must not overlap");
+  return launched(
+      ci8::launch_silu_mul_quantize(x, codes, scales, int(m), int(k), as_stream(stream)));
+}
+
 }  // extern "C"

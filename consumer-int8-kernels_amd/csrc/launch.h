@@ -27,6 +27,12 @@ hipError_t launch_grouped_summed_gemm(const int8_t* a, const int8_t* w, const fl
                                       const void* sw, void* out, int groups, int m, int n,
                                       int k, hipStream_t stream);
 
+// x BF16 [m, 2k] = [gate | up] -> out BF16 [m, k] = bf16(silu(gate) * up).
+hipError_t launch_silu_mul(const void* x, void* out, int m, int k, hipStream_t stream);
+// The same activations quantized per row like launch_quantize_rows, never written out.
+hipError_t launch_silu_mul_quantize(const void* x, int8_t* codes, float* scales, int m, int k,
+                                    hipStream_t stream);
+
 hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale, void* out,
                                int m, int n, int k, hipStream_t stream);
 

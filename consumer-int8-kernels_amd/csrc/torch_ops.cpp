@@ -12,6 +12,7 @@
 #include <torch/csrc/stable/tensor.h>
 #include <torch/headeronly/util/Exception.h>
 
+#include <climits>
 #include <string>
 
 #include "consumer_int8_amd.h"
@@ -183,9 +184,42 @@ void channel_gemv(Tensor x, Tensor w, Tensor scale, Tensor out) {
                                   stream_for(device)));
 }
 
+// csrc/bindings.cpp:32-44
+void silu_mul(Tensor x, Tensor out) {
+  const int device = x.get_device_index();
+  check(x, ScalarType::BFloat16, device);
+  check(out, ScalarType::BFloat16, device);
+  STD_TORCH_CHECK(x.dim() == 2 && out.dim() == 2 &&
+                      (out.size(1) == 8704 || out.size(1) == 17408) &&
+                      x.size(1) == 2 * out.size(1) && x.size(0) == out.size(0) &&
+                      x.numel() <= INT_MAX,
+                  "Unsupported SwiGLU shape");
+  torch::stable::accelerator::DeviceGuard guard(device);
+  raise_on_error(ci8_silu_mul(x.data_ptr(), out.data_ptr(), x.size(0), out.size(1),
+                              stream_for(device)));
+}
+
+// csrc/bindings.cpp:46-64
+void silu_mul_quantize(Tensor x, Tensor codes, Tensor scales) {
+  const int device = x.get_device_index();
+  check(x, ScalarType::BFloat16, device);
+  check(codes, ScalarType::Char, device);
+  check(scales, ScalarType::Float, device);
+  STD_TORCH_CHECK(x.dim() == 2 && codes.dim() == 2 && scales.dim() == 1 &&
+                      (codes.size(1) == 8704 || codes.size(1) == 17408) &&
+                      x.size(1) == 2 * codes.size(1) && x.size(0) == codes.size(0) &&
+                      scales.size(0) == x.size(0) && x.numel() <= INT_MAX,
+                  "Unsupported SwiGLU quantization shape");
+  torch::stable::accelerator::DeviceGuard guard(device);
+  raise_on_error(ci8_silu_mul_quantize(x.data_ptr(), static_cast<int8_t*>(codes.data_ptr()),
+                                       static_cast<float*>(scales.data_ptr()), x.size(0),
+                                       codes.size(1), stream_for(device)));
+}
+
 }  // namespace
 
-// Schemas: csrc/bindings.cpp:598, 603-606, 610; grouped_summed_mm has no reference op.
+// Schemas: csrc/bindings.cpp:594-595, 598, 603-606, 610; grouped_summed_mm has no
+// reference op.
 STABLE_TORCH_LIBRARY(consumer_int8, m) {
   m.def("fused_channel_mm(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) out, int schedule=0) -> ()");
   m.def("quantize_rows(Tensor input, Tensor(a!) codes, Tensor(b!) scales) -> ()");
@@ -194,6 +228,8 @@ STABLE_TORCH_LIBRARY(consumer_int8, m) {
   m.def("channel_gemv(Tensor x, Tensor w, Tensor scale, Tensor(a!) out) -> ()");
   m.def("cutlass_channel_mm(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) workspace, Tensor(b!) out) -> ()");
   m.def("grouped_summed_mm(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) out) -> ()");
+  m.def("silu_mul(Tensor input, Tensor(a!) out) -> ()");
+  m.def("silu_mul_quantize(Tensor input, Tensor(a!) codes, Tensor(b!) scales) -> ()");
 }
 
 // HIP tensors carry the CUDA dispatch key in PyTorch-ROCm.
@@ -205,6 +241,8 @@ STABLE_TORCH_LIBRARY_IMPL(consumer_int8, CUDA, m) {
   m.impl("channel_gemv", TORCH_BOX(&channel_gemv));
   m.impl("cutlass_channel_mm", TORCH_BOX(&cutlass_channel_mm));
   m.impl("grouped_summed_mm", TORCH_BOX(&grouped_summed_mm));
+  m.impl("silu_mul", TORCH_BOX(&silu_mul));
+  m.impl("silu_mul_quantize", TORCH_BOX(&silu_mul_quantize));
 }
 
 extern "C" PyObject* PyInit__C() {

@@ -19,6 +19,8 @@
  *   ci8_grouped_summed_mm    no reference op (configs[4]'s summed grouped W8A8); the
  *                            closest reference code is benchmarks/cuda/q8_block_int8.cu:54-55
  *   ci8_channel_gemv         csrc/kernels.h:54-55, csrc/bindings.cpp:289-310, schema :606
+ *   ci8_silu_mul             csrc/silu_quant.h:8, csrc/bindings.cpp:32-44, schema :594
+ *   ci8_silu_mul_quantize    csrc/silu_quant.h:6-7, csrc/bindings.cpp:46-64, schema :595
  */
 #ifndef CONSUMER_INT8_AMD_H
 #define CONSUMER_INT8_AMD_H
@@ -119,6 +121,24 @@ int ci8_grouped_summed_mm(const int8_t* a, const int8_t* w, const float* a_scale
  *           int k, cudaStream_t), csrc/kernels.h:54-55; checks of csrc/bindings.cpp:298-305. */
 int ci8_channel_gemv(const void* x, const int8_t* w, const void* scale, void* out,
                      int64_t m, int64_t n, int64_t k, void* stream);
+
+/* silu_mul: x BF16 [m,2k] (gate in columns [0,k), up in [k,2k)) -> out BF16 [m,k] =
+ * bf16_rn(fl(fl(g / fl(1 + exp(-g))) * u)) in FP32 with IEEE division and an exp within
+ * one ULP. Requires k in {8704, 17408}, m >= 0 (0 is a no-op) and 2*m*k <= INT_MAX;
+ * any 2-byte alignment; x and out must not overlap.
+ * Replaces: silu_mul(const void*, void*, int m, int k, cudaStream_t),
+ *           csrc/silu_quant.h:8; checks of csrc/bindings.cpp:36-40. */
+int ci8_silu_mul(const void* x, void* out, int64_t m, int64_t k, void* stream);
+
+/* silu_mul_quantize: the silu_mul activations of x BF16 [m,2k], quantized per row as
+ * ci8_quantize_rows does, without writing them: codes INT8 [m,k], scales FP32 [m].
+ * codes and scales equal ci8_quantize_rows applied to ci8_silu_mul's output, bit for bit.
+ * Requires k in {8704, 17408}, m >= 0 (0 is a no-op), 2*m*k <= INT_MAX, x 16-byte,
+ * codes 8-byte and scales 4-byte aligned, and no overlap between the three buffers.
+ * Replaces: silu_mul_quantize(const void*, int8_t*, float*, int m, int k, cudaStream_t),
+ *           csrc/silu_quant.h:6-7; checks of csrc/bindings.cpp:51-59. */
+int ci8_silu_mul_quantize(const void* x, int8_t* codes, float* scales, int64_t m, int64_t k,
+                          void* stream);
 
 #ifdef __cplusplus
 }

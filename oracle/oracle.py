@@ -1,8 +1,8 @@
 """CPU oracle for the INT8 linear-layer hot path -- TEST INFRASTRUCTURE ONLY.
 
 This module restates, in numpy, the arithmetic of AppMana/consumer-int8-kernels for
-quantize_rows, quantize_grouped4096, fused/cutlass_channel_mm, channel_mm, channel_gemv
-and the channel weight encoding. Only tests/, __graft_entry__.smoke() and bench.py's
+quantize_rows, quantize_grouped4096, fused/cutlass_channel_mm, channel_mm, channel_gemv,
+the channel weight encoding and the SwiGLU producers silu_mul / silu_mul_quantize. Only tests/, __graft_entry__.smoke() and bench.py's
 cpu_baseline leg may import it, and only as the checker (or the timed CPU baseline);
 the product path never calls it and has no CPU fallback.
 
@@ -88,6 +88,94 @@ def quantize_grouped4096(x_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     assert k == 4096
     codes, scales = quantize_rows(np.ascontiguousarray(x_bits.transpose(1, 0, 2)).reshape(g * m, k))
     return codes.reshape(g, m, k), scales.reshape(g, m)
+
+
+# ---------------------------------------------------------------- SwiGLU
+
+# ln(FLT_MAX): e^x overflows FP32 above this (e^-g for gate g <= -89 in BF16).
+EXP_F32_OVERFLOW = float(np.log(np.float64(np.finfo(np.float32).max)))
+# Relative error budget of an FP32 evaluation of silu(g) * u before its BF16 rounding:
+# exp and reciprocal (or division) each within 2 ULP plus three correctly rounded FP32
+# operations stay below 2^-20 (one ULP is at most 2^-23 relative).
+SILU_REL = 2.0**-20
+
+
+def round_bf16_f64(values: np.ndarray) -> np.ndarray:
+    """float64 -> nearest BF16 value (ties to even) as float64, in one rounding.
+
+    BF16 has 8 significand bits, exponents down to 2^-126 (subnormal spacing 2^-133)
+    and overflows to infinity at (2 - 2^-8) * 2^127. NaN and infinities pass through.
+    """
+    v = np.asarray(values, dtype=np.float64)
+    finite = np.isfinite(v)
+    safe = np.where(finite, v, 0.0)
+    _, e = np.frexp(safe)
+    e = np.maximum(e, -125)
+    r = np.ldexp(np.rint(np.ldexp(safe, 8 - e)), e - 8)
+    r = np.where(np.abs(r) >= 2.0**128, np.copysign(np.inf, r), r)
+    return np.where(finite, r, v)
+
+
+def silu_mul_exact(x_bits: np.ndarray) -> np.ndarray:
+    """SwiGLU of BF16 x [M, 2K] = [gate | up] as float64 values [M, K].
+
+    csrc/silu_quant.cu:27-31 and :69-71: gate = x[:, :K], up = x[:, K:], silu(g) =
+    g / (1 + e^-g) and value = silu(g) * up, in FP32, then rounded to BF16. Here the
+    value is computed in float64 (exact up to float64 rounding), keeping the one FP32
+    effect that moves a result by more than SILU_REL: e^-g overflows FP32 for
+    -g > ln(FLT_MAX), and the FP32 quotient g / inf is then -0.
+    """
+    with np.errstate(over="ignore", invalid="ignore"):
+        x = bf16_to_f32(x_bits).astype(np.float64)  # signalling NaNs raise "invalid"
+        k = x.shape[-1] // 2
+        g, u = x[..., :k], x[..., k:]
+        e = np.where(-g > EXP_F32_OVERFLOW, np.inf, np.exp(-g))
+        return g / (1.0 + e) * u
+
+
+def silu_mul(x_bits: np.ndarray) -> np.ndarray:
+    """silu_mul (csrc/silu_quant.cu:63-72, :83-88): BF16 bits [M, K], the BF16 value
+    nearest the exact SwiGLU."""
+    return f32_to_bf16(round_bf16_f64(silu_mul_exact(x_bits)).astype(np.float32))
+
+
+def silu_mul_bounds(x_bits: np.ndarray, rel: float = SILU_REL) -> tuple[np.ndarray, np.ndarray]:
+    """Interval [lo, hi] (float64, per element) holding the BF16 output of any FP32
+    evaluation whose pre-rounding value p satisfies |p - v| <= rel*|v| + 2^-126 for the
+    exact value v. BF16 rounding is monotonic, so bf16(v - d) <= bf16(p) <= bf16(v + d)
+    with d = rel*|v| + 2^-126 (the absolute term admits FP32 subnormal flushing). Where
+    v is infinite or NaN the interval is [v, v]. lo == hi except where v lies within d
+    of a BF16 rounding midpoint.
+    """
+    v = silu_mul_exact(x_bits)
+    with np.errstate(invalid="ignore"):
+        d = rel * np.abs(v) + 2.0**-126
+        lo = round_bf16_f64(v - d)
+        hi = round_bf16_f64(v + d)
+    special = ~np.isfinite(v)
+    return np.where(special, v, lo), np.where(special, v, hi)
+
+
+def within_bounds(got_bits: np.ndarray, lo: np.ndarray, hi: np.ndarray) -> np.ndarray:
+    """Elementwise: BF16 `got_bits` lies in [lo, hi]; NaN matches NaN."""
+    got = bf16_to_f32(got_bits).astype(np.float64)
+    both_nan = np.isnan(got) & np.isnan(lo)
+    with np.errstate(invalid="ignore"):
+        return both_nan | ((got >= lo) & (got <= hi))
+
+
+def silu_mul_quantize(x_bits: np.ndarray, activations: np.ndarray | None = None):
+    """silu_mul_quantize (csrc/silu_quant.cu:10-60): (codes [M, K], scales [M]).
+
+    The BF16 activations are quantized per row with quantize_rows' arithmetic
+    (:32-43 max of |value| from 0, :44 scale = max(amax/127, 1e-20), :55-56 code =
+    clamp(rne(value/scale), -127, 127)). `activations` (BF16 bits) replaces the
+    nearest-BF16 SwiGLU, for checking a producer whose values differ from it only
+    within silu_mul_bounds.
+    """
+    if activations is None:
+        activations = silu_mul(x_bits)
+    return quantize_rows(activations)
 
 
 # ---------------------------------------------------------------- W8A8 GEMMs

@@ -21,7 +21,7 @@ def test_header_declares_the_expected_entry_points():
     assert declared_functions() == sorted([
         "ci8_last_error", "ci8_version", "ci8_quantize_rows", "ci8_quantize_grouped4096",
         "ci8_fused_channel_mm", "ci8_cutlass_channel_mm", "ci8_channel_mm",
-        "ci8_channel_gemv", "ci8_grouped_summed_mm",
+        "ci8_channel_gemv", "ci8_grouped_summed_mm", "ci8_silu_mul", "ci8_silu_mul_quantize",
     ])
 
 
@@ -128,6 +128,27 @@ def test_grouped_summed_rejections(lib):
                                           None), A.CI8_ERR_TOO_LARGE, "Matrix too large")
 
 
+def test_swiglu_rejections(lib):
+    """csrc/bindings.cpp:36-40 and :51-59: the two widths, the INT_MAX bound, and the
+    quantizing op's 16-byte input and 8-byte code alignment."""
+    from consumer_int8 import _abi as A
+
+    for m, k in [(-1, 8704), (4, 4096), (4, 8703), (4, 17409), (1 << 17, 17408)]:
+        expect(lib, lib.ci8_silu_mul(FAKE, FAKE, m, k, None), A.CI8_ERR_GEOMETRY,
+               "Unsupported SwiGLU shape")
+        expect(lib, lib.ci8_silu_mul_quantize(FAKE, FAKE, FAKE, m, k, None),
+               A.CI8_ERR_GEOMETRY, "Unsupported SwiGLU quantization shape")
+    expect(lib, lib.ci8_silu_mul(FAKE + 1, FAKE, 4, 8704, None), A.CI8_ERR_ALIGNMENT,
+           "aligned buffers")
+    for x, codes in [(FAKE + 2, FAKE), (FAKE + 8, FAKE), (FAKE, FAKE + 4)]:
+        expect(lib, lib.ci8_silu_mul_quantize(x, codes, FAKE, 4, 8704, None),
+               A.CI8_ERR_ALIGNMENT, "SwiGLU quantization requires aligned buffers")
+    expect(lib, lib.ci8_silu_mul(FAKE, FAKE + 4 * 8704, 4, 8704, None), A.CI8_ERR_OVERLAP,
+           "must not overlap")
+    expect(lib, lib.ci8_silu_mul_quantize(FAKE, FAKE + (1 << 20), FAKE + 64, 4, 8704, None),
+           A.CI8_ERR_OVERLAP, "must not overlap")
+
+
 def test_torch_surface_matches_reference_schemas():
     import torch
 
@@ -142,6 +163,8 @@ def test_torch_surface_matches_reference_schemas():
         "cutlass_channel_mm": "(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) workspace, Tensor(b!) out) -> ()",
         # no reference counterpart (configs[4]'s summed grouped W8A8)
         "grouped_summed_mm": "(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) out) -> ()",
+        "silu_mul": "(Tensor input, Tensor(a!) out) -> ()",
+        "silu_mul_quantize": "(Tensor input, Tensor(a!) codes, Tensor(b!) scales) -> ()",
     }
     for name, schema in expected.items():
         handle = getattr(ops, name)
@@ -174,3 +197,8 @@ def test_fake_tensor_registration():
         sw = torch.empty(8, dtype=torch.bfloat16)
         out = torch.empty(4, 8, dtype=torch.bfloat16)
         assert ops.fused_channel_mm(a, w, sa, sw, out, 0) is None
+        x = torch.empty(2, 2 * 8704, dtype=torch.bfloat16)
+        act = torch.empty(2, 8704, dtype=torch.bfloat16)
+        codes = torch.empty(2, 8704, dtype=torch.int8)
+        assert ops.silu_mul(x, act) is None
+        assert ops.silu_mul_quantize(x, codes, torch.empty(2)) is None

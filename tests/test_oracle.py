@@ -286,3 +286,112 @@ def test_quantize_channel_rejects_nonfinite_and_matches_exact():
             q = max(-128, min(127, E.rne_int(E.f32(Fraction(float(w[i, t])) / s))))
             assert int(codes[i, t]) == q + 128
         assert int(scale_bits[i]) == E.bf16_bits(float(E.bf16(s)))
+
+
+# ------------------------------------------------------------------ SwiGLU
+
+def swiglu_bits(gate, up):
+    """BF16 x [M, 2K] = [gate | up] from float values that are exact in BF16."""
+    return np.concatenate([bf16_from_f32(gate), bf16_from_f32(up)], axis=-1)
+
+
+def test_round_bf16_f64_matches_exact_rational_rounding():
+    """Midpoints, near-midpoints, subnormals and the overflow edge against
+    tests/exact.py's hand-written round-half-to-even."""
+    vals = O.bf16_to_f32(all_finite_bf16()).astype(np.float64)
+    vals = np.unique(np.abs(vals))
+    mids = (vals[:-1] + vals[1:]) / 2
+    rng = np.random.default_rng(21)
+    cases = np.concatenate([mids, mids * (1 + 2.0**-40), mids * (1 - 2.0**-40),
+                            rng.standard_normal(4000) * 10.0 ** rng.uniform(-40, 38, 4000)])
+    cases = rng.choice(cases, 6000, replace=False)
+    cases = np.concatenate([cases, -cases, [3.3961e38, 3.3963e38, 1e-45, 2.0**-134]])
+    got = O.round_bf16_f64(cases)
+    for v, g in zip(cases, got):
+        want = E.bf16(Fraction(float(v)))
+        assert float(want) == g, (v, g, want)
+
+
+def test_silu_mul_known_answers():
+    """Closed forms: silu(0) = 0, silu(1) = 1/(1 + 1/e), silu(g) -> g for large g, and
+    the FP32 overflow of e^-g for g <= -89 (the quotient is then -0)."""
+    gate = np.array([[0.0, 1.0, 100.0, -89.0, 2.0, -1.0]], np.float32)
+    up = np.array([[5.0, 1.0, 1.0, 1.0, -3.0, 1.0]], np.float32)
+    x = swiglu_bits(gate, up)
+    exact = O.silu_mul_exact(x)
+    assert exact[0, 0] == 0.0
+    assert exact[0, 1] == pytest.approx(1.0 / (1.0 + np.exp(-1.0)), rel=1e-15)
+    assert exact[0, 2] == 100.0
+    assert exact[0, 3] == 0.0 and np.signbit(exact[0, 3])
+    assert exact[0, 4] == pytest.approx(-3.0 * 2.0 / (1.0 + np.exp(-2.0)), rel=1e-15)
+    bits = O.silu_mul(x)
+    # 0.7310585786 / 2^-8 = 187.15 -> 187 * 2^-8 = 0.73046875 = 0x3F3B
+    assert int(bits[0, 1]) == 0x3F3B
+    assert int(bits[0, 2]) == E.bf16_bits(100.0)
+    # -0.2689414214 (silu(-1)): 2^-9 spacing in [0.25, 0.5): 137.70 -> 138 * 2^-9
+    assert O.bf16_to_f32(bits[0, 5:6])[0] == np.float32(-138 * 2.0**-9)
+
+
+def test_silu_mul_matches_independent_sigmoid_and_identity():
+    """silu(g) * u = g * expit(g) * u (scipy's logistic, a separate implementation), and
+    silu(g) - silu(-g) = g; a swapped gate/up, a sign slip in the exponent or a missing
+    factor fails one of them."""
+    from scipy.special import expit
+
+    rng = np.random.default_rng(31)
+    g = O.bf16_to_f32(O.f32_to_bf16((rng.standard_normal((3, 64)) * 6).astype(np.float32)))
+    u = O.bf16_to_f32(O.f32_to_bf16(rng.standard_normal((3, 64)).astype(np.float32)))
+    exact = O.silu_mul_exact(swiglu_bits(g, u))
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    assert np.allclose(exact, g64 * expit(g64) * u64, rtol=1e-14, atol=0)
+    ones = np.ones_like(g)
+    pos = O.silu_mul_exact(swiglu_bits(g, ones))
+    neg = O.silu_mul_exact(swiglu_bits(-g, ones))
+    assert np.allclose(pos - neg, g64, rtol=1e-13, atol=1e-13)
+
+
+def test_silu_mul_bounds_contain_fp32_evaluations_and_reject_planted_mistakes():
+    """The tolerance interval holds an FP32 step-by-step evaluation (correctly rounded
+    exp, division and product), is a single BF16 value for almost every element, and
+    excludes the outputs of plausible mistakes planted in a copy of the formula."""
+    rng = np.random.default_rng(41)
+    x = O.f32_to_bf16((rng.standard_normal((8, 2 * 8704)) * 3).astype(np.float32))
+    lo, hi = O.silu_mul_bounds(x)
+    assert np.mean(lo != hi) < 2e-3
+    assert np.all(O.within_bounds(O.silu_mul(x), lo, hi))
+
+    f = O.bf16_to_f32(x)
+    g, u = f[:, :8704], f[:, 8704:]
+    e = np.exp(-g.astype(np.float64)).astype(np.float32)
+    d = (np.float32(1) + e).astype(np.float32)
+    p = ((g / d).astype(np.float32) * u).astype(np.float32)
+    assert np.all(O.within_bounds(O.f32_to_bf16(p), lo, hi))
+
+    def fraction_outside(values):
+        return np.mean(~O.within_bounds(O.f32_to_bf16(values.astype(np.float32)), lo, hi))
+
+    assert fraction_outside(g / (1 + np.exp(g)) * u) > 0.5           # sign slip
+    assert fraction_outside(u / (1 + np.exp(-u)) * g) > 0.5          # gate and up swapped
+    assert fraction_outside(g / (1 + np.exp(-g))) > 0.5              # product dropped
+    bf16_silu = O.bf16_to_f32(O.f32_to_bf16((g / d).astype(np.float32)))
+    assert fraction_outside(bf16_silu * u) > 0.01                    # extra BF16 rounding
+
+
+def test_silu_mul_quantize_is_quantize_rows_of_the_activations():
+    """csrc/silu_quant.cu:32-56 quantizes the BF16-rounded values with quantize_rows'
+    arithmetic; a zero row (tests/test_cuda_ops.py:884) gets scale 1e-20 and zero codes."""
+    rng = np.random.default_rng(51)
+    x = O.f32_to_bf16((rng.standard_normal((5, 2 * 8704)) * 3).astype(np.float32))
+    x[0] = 0
+    codes, scales = O.silu_mul_quantize(x)
+    ref_codes, ref_scales = O.quantize_rows(O.silu_mul(x))
+    assert np.array_equal(codes, ref_codes) and np.array_equal(scales, ref_scales)
+    assert scales[0] == np.float32(1e-20) and not codes[0].any()
+    act = O.bf16_to_f32(O.silu_mul(x)[1:]).astype(np.float64)
+    amax = np.abs(act).max(axis=1)
+    assert np.array_equal(scales[1:], np.maximum((amax / 127).astype(np.float32), np.float32(1e-20)))
+    for r in range(1, 5):
+        s = E.f32(Fraction(float(amax[r - 1])) / 127)
+        for t in rng.choice(8704, 40, replace=False):
+            q = E.rne_int(E.f32(Fraction(float(act[r - 1, t])) / s))
+            assert int(codes[r, t]) == max(-127, min(127, q))
