@@ -11,8 +11,9 @@ rotate over enough copies that no step finds its inputs in the 256 MB Infinity C
 Also reported: `roofline` for the dominant kernel (the GEMM, timed per launch with HIP
 events on the stream it runs on); extra roofline lines for the quantizer, the W8A16
 GEMV, the grouped summed GEMM, the biased-UINT8 down
-projection and its SwiGLU activation producers (silu_mul_quantize,
-silu_mul), and the small quantize + GEMM pass; and
+projection with its SwiGLU activation producers (silu_mul_quantize,
+silu_mul) and the AllSpark weight restore (unpack_allspark), and the small quantize +
+GEMM pass (configs[0]); and
 `cpu_baseline`, the CPU oracle on a bounded row slice of the same workload on this
 host's cores.
 
@@ -317,6 +318,23 @@ def main() -> int:
                                    "frac": round(bs / (mean_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
                                    "mean_us": round(mean_us, 2), "bytes": bs}
         del xs, act
+        # unpack_allspark of configs[3]'s weights [5120, 17408]: 3 packed copies rotate
+        # (267 MB of input plus the 89 MB output exceed the MALL).
+        pk = [torch.randint(0, 256, (N4, K4), generator=gen, device="cuda", dtype=torch.uint8)
+              for _ in range(3)]
+        pks = torch.randn(N4, generator=gen, device="cuda").to(torch.bfloat16)
+        wu = torch.empty(N4, K4, device="cuda", dtype=torch.int8)
+        su = torch.empty(N4, device="cuda", dtype=torch.bfloat16)
+        calls = [lambda i=i: ops.unpack_allspark(pk[i], pks, wu, su) for i in range(3)]
+        for c in calls:
+            c()
+        mean_us, _ = time_kernel(torch, calls, 6)
+        bu = 2 * N4 * K4 + 4 * N4
+        extras["unpack_allspark_cfg4"] = {"bound": "hbm", "achieved": round(bu / (mean_us * 1e-6) / 1e9, 1),
+                                          "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                          "frac": round(bu / (mean_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                                          "mean_us": round(mean_us, 2), "bytes": bu}
+        del pk, pks, wu, su
         # quantize_rows + fused_channel_mm at M=128, K=4096, N=4096; AI 234
         # op/B is below the ridge, so this small case is bounded by HBM (bytes below).
         M1, K1, N1 = 128, 4096, 4096

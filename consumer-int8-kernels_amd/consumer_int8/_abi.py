@@ -34,6 +34,7 @@ SIGNATURES = {
     "ci8_grouped_summed_mm": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p], ctypes.c_int),
     "ci8_silu_mul": ([_p, _p, _i64, _i64, _p], ctypes.c_int),
     "ci8_silu_mul_quantize": ([_p, _p, _p, _i64, _i64, _p], ctypes.c_int),
+    "ci8_unpack_allspark": ([_p, _p, _p, _p, _i64, _i64, _p], ctypes.c_int),
 }
 
 _lib = None

@@ -32,6 +32,9 @@ silu_mul(input, out)
 silu_mul_quantize(input, codes, scales)
     The silu_mul activations quantized per row exactly as quantize_rows, without
     writing them out: codes INT8 [M,K], scales FP32 [M].
+unpack_allspark(packed, packed_scales, weight, scales)
+    AllSpark N32K16 UINT8 [ceil(N/32)*32, K] weights and permuted BF16 scales ->
+    row-major signed INT8 [N, K] (code = byte - 128) and BF16 [N], losslessly; N % 16 == 0.
 """
 
 import torch
@@ -47,6 +50,7 @@ fused_channel_mm = torch.ops.consumer_int8.fused_channel_mm
 grouped_summed_mm = torch.ops.consumer_int8.grouped_summed_mm
 silu_mul = torch.ops.consumer_int8.silu_mul
 silu_mul_quantize = torch.ops.consumer_int8.silu_mul_quantize
+unpack_allspark = torch.ops.consumer_int8.unpack_allspark
 
 
 @torch.library.register_fake("consumer_int8::fused_channel_mm")
@@ -91,4 +95,9 @@ def _silu_mul_fake(input, out):
 
 @torch.library.register_fake("consumer_int8::silu_mul_quantize")
 def _silu_mul_quantize_fake(input, codes, scales):
+    return None
+
+
+@torch.library.register_fake("consumer_int8::unpack_allspark")
+def _unpack_allspark_fake(packed, packed_scales, weight, scales):
     return None

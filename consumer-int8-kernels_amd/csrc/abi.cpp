@@ -181,4 +181,23 @@ int ci8_silu_mul_quantize(const void* x, int8_t* codes, float* scales, int64_t m
       ci8::launch_silu_mul_quantize(x, codes, scales, int(m), int(k), as_stream(stream)));
 }
 
+// csrc/bindings.cpp:276-284
+int ci8_unpack_allspark(const uint8_t* packed, const void* packed_scales, int8_t* weight,
+                        void* scales, int64_t n, int64_t k, void* stream) {
+  if (!(n > 0 && n % 16 == 0 && k > 0 && k <= 65536 && k % 16 == 0))
+    return fail(CI8_ERR_GEOMETRY, "Expected AllSpark N32K16 weights and channel scales");
+  const int64_t padded_n = (n + 31) / 32 * 32;
+  if (padded_n * k > INT_MAX) return fail(CI8_ERR_TOO_LARGE, "Weight too large");
+  if (!aligned(packed, 4) || !aligned(weight, 16) || !aligned(packed_scales, 2) ||
+      !aligned(scales, 2))
+    return fail(CI8_ERR_ALIGNMENT, "Unaligned weights");
+  if (overlap(packed, padded_n * k, weight, n * k) ||
+      overlap(packed, padded_n * k, scales, n * 2) ||
+      overlap(packed_scales, padded_n * 2, weight, n * k) ||
+      overlap(packed_scales, padded_n * 2, scales, n * 2) || overlap(weight, n * k, scales, n * 2))
+    return fail(CI8_ERR_OVERLAP, "AllSpark buffers must not overlap");
+  return launched(ci8::launch_unpack_allspark(packed, packed_scales, weight, scales, int(n),
+                                              int(k), as_stream(stream)));
+}
+
 }  // extern "C"

@@ -33,6 +33,13 @@ hipError_t launch_silu_mul(const void* x, void* out, int m, int k, hipStream_t s
 hipError_t launch_silu_mul_quantize(const void* x, int8_t* codes, float* scales, int m, int k,
                                     hipStream_t stream);
 
+// AllSpark N32K16 packed [ceil(n/32)*32, k] UINT8 + permuted BF16 scales -> row-major
+// signed INT8 [n, k] + BF16 [n]. Requires n % 16 == 0, k % 16 == 0, packed 4-byte and
+// weight 16-byte aligned.
+hipError_t launch_unpack_allspark(const uint8_t* packed, const void* packed_scales,
+                                  int8_t* weight, void* scales, int n, int k,
+                                  hipStream_t stream);
+
 hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale, void* out,
                                int m, int n, int k, hipStream_t stream);
 

@@ -216,9 +216,31 @@ void silu_mul_quantize(Tensor x, Tensor codes, Tensor scales) {
                                        codes.size(1), stream_for(device)));
 }
 
+// csrc/bindings.cpp:266-288
+void unpack_allspark(Tensor packed, Tensor packed_scales, Tensor weight, Tensor scales) {
+  const int device = packed.get_device_index();
+  check(packed, ScalarType::Byte, device);
+  check(packed_scales, ScalarType::BFloat16, device);
+  check(weight, ScalarType::Char, device);
+  check(scales, ScalarType::BFloat16, device);
+  STD_TORCH_CHECK(packed.dim() == 2 && weight.dim() == 2 && packed_scales.dim() == 1 &&
+                      scales.dim() == 1,
+                  "Wrong tensor ranks");
+  const int64_t n = weight.size(0), k = weight.size(1), padded_n = (n + 31) / 32 * 32;
+  STD_TORCH_CHECK(n > 0 && n % 16 == 0 && k > 0 && k <= 65536 && k % 16 == 0 &&
+                      packed.size(0) == padded_n && packed.size(1) == k &&
+                      packed_scales.size(0) == padded_n && scales.size(0) == n,
+                  "Expected AllSpark N32K16 weights and channel scales");
+  torch::stable::accelerator::DeviceGuard guard(device);
+  raise_on_error(ci8_unpack_allspark(static_cast<uint8_t*>(packed.data_ptr()),
+                                     packed_scales.data_ptr(),
+                                     static_cast<int8_t*>(weight.data_ptr()), scales.data_ptr(),
+                                     n, k, stream_for(device)));
+}
+
 }  // namespace
 
-// Schemas: csrc/bindings.cpp:594-595, 598, 603-606, 610; grouped_summed_mm has no
+// Schemas: csrc/bindings.cpp:594-595, 598, 603-607, 610; grouped_summed_mm has no
 // reference op.
 STABLE_TORCH_LIBRARY(consumer_int8, m) {
   m.def("fused_channel_mm(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) out, int schedule=0) -> ()");
@@ -230,6 +252,7 @@ STABLE_TORCH_LIBRARY(consumer_int8, m) {
   m.def("grouped_summed_mm(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) out) -> ()");
   m.def("silu_mul(Tensor input, Tensor(a!) out) -> ()");
   m.def("silu_mul_quantize(Tensor input, Tensor(a!) codes, Tensor(b!) scales) -> ()");
+  m.def("unpack_allspark(Tensor packed, Tensor packed_scales, Tensor(a!) weight, Tensor(b!) scales) -> ()");
 }
 
 // HIP tensors carry the CUDA dispatch key in PyTorch-ROCm.
@@ -243,6 +266,7 @@ STABLE_TORCH_LIBRARY_IMPL(consumer_int8, CUDA, m) {
   m.impl("grouped_summed_mm", TORCH_BOX(&grouped_summed_mm));
   m.impl("silu_mul", TORCH_BOX(&silu_mul));
   m.impl("silu_mul_quantize", TORCH_BOX(&silu_mul_quantize));
+  m.impl("unpack_allspark", TORCH_BOX(&unpack_allspark));
 }
 
 extern "C" PyObject* PyInit__C() {

@@ -21,6 +21,8 @@
  *   ci8_channel_gemv         csrc/kernels.h:54-55, csrc/bindings.cpp:289-310, schema :606
  *   ci8_silu_mul             csrc/silu_quant.h:8, csrc/bindings.cpp:32-44, schema :594
  *   ci8_silu_mul_quantize    csrc/silu_quant.h:6-7, csrc/bindings.cpp:46-64, schema :595
+ *   ci8_unpack_allspark      csrc/kernels.h:52-53, csrc/bindings.cpp:266-288,
+ *                            schema :607
  */
 #ifndef CONSUMER_INT8_AMD_H
 #define CONSUMER_INT8_AMD_H
@@ -139,6 +141,19 @@ int ci8_silu_mul(const void* x, void* out, int64_t m, int64_t k, void* stream);
  *           csrc/silu_quant.h:6-7; checks of csrc/bindings.cpp:51-59. */
 int ci8_silu_mul_quantize(const void* x, int8_t* codes, float* scales, int64_t m, int64_t k,
                           void* stream);
+
+/* unpack_allspark: AllSpark N32K16 packed weights -> row-major signed INT8 weights and
+ * channel scales, losslessly. packed UINT8 [padded_n,k] (padded_n = n rounded up to a
+ * multiple of 32) holds biased codes (code + 128) in the N32K16 tile order;
+ * packed_scales BF16 [padded_n] holds the scales permuted within each group of 32.
+ * Writes weight INT8 [n,k] = code and scales BF16 [n]. Padding rows are never read.
+ * Requires n > 0, n % 16 == 0, 0 < k <= 65536, k % 16 == 0, padded_n*k <= INT_MAX,
+ * packed 4-byte and weight 16-byte aligned, and no overlap between the four buffers.
+ * Replaces: unpack_allspark(const uint8_t*, const void*, int8_t*, void*, int n, int k,
+ *           cudaStream_t), csrc/allspark_layout.cu:30-35; checks of
+ *           csrc/bindings.cpp:276-284. */
+int ci8_unpack_allspark(const uint8_t* packed, const void* packed_scales, int8_t* weight,
+                        void* scales, int64_t n, int64_t k, void* stream);
 
 #ifdef __cplusplus
 }

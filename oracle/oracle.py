@@ -2,7 +2,8 @@
 
 This module restates, in numpy, the arithmetic of AppMana/consumer-int8-kernels for
 quantize_rows, quantize_grouped4096, fused/cutlass_channel_mm, channel_mm, channel_gemv,
-the channel weight encoding and the SwiGLU producers silu_mul / silu_mul_quantize. Only tests/, __graft_entry__.smoke() and bench.py's
+the channel weight encoding, the SwiGLU producers silu_mul / silu_mul_quantize and the
+AllSpark N32K16 weight layout (unpack_allspark, with its inverse packer). Only tests/, __graft_entry__.smoke() and bench.py's
 cpu_baseline leg may import it, and only as the checker (or the timed CPU baseline);
 the product path never calls it and has no CPU fallback.
 
@@ -292,6 +293,60 @@ def bf16_ulp(values: np.ndarray) -> np.ndarray:
     exp = np.floor(np.log2(np.where(v > 0, v, 2.0**-126)))
     exp = np.maximum(exp, -126)
     return 2.0 ** (exp - 7)
+
+
+# ---------------------------------------------------------------- AllSpark N32K16
+
+def allspark_padded_rows(n: int) -> int:
+    """Packed rows of an N32K16 weight: n rounded up to 32 (csrc/bindings.cpp:276)."""
+    return (n + 31) // 32 * 32
+
+
+def allspark_unpack_index(n: int, k: int) -> tuple[np.ndarray, np.ndarray]:
+    """(byte_index [n, k], scale_index [n]): where weight[row, col] and scale[row] are
+    read from the flat packed buffers, restated from csrc/allspark_layout.cu:10-26:
+
+      packed_row = (row / 32) * 8 + row % 8                                   :14
+      word       = packed_row * 4k + tile * 64 + ((row % 32) / 16) * 8
+                   + ((row % 16) / 8) * 4,  tile = col / 16                   :15-16
+      words a, b, c, d at word + 0, 16, 32, 48 bytes                          :17-18
+      restored bytes of the tile: a0 a1 b0 b1 c0 c1 d0 d1 a2 a3 b2 b3 c2 c3 d2 d3  :20-23
+      scale      = packed_scales[(row / 32) * 32 + (row % 8) * 4 + (row % 32) / 8]   :26
+    """
+    row = np.arange(n, dtype=np.int64)[:, None]
+    col = np.arange(k, dtype=np.int64)[None, :]
+    packed_row = (row // 32) * 8 + row % 8
+    word = packed_row * 4 * k + (col // 16) * 64 + ((row % 32) // 16) * 8 + ((row % 16) // 8) * 4
+    c = col % 16
+    # position c of the restored 16 bytes: word (c % 8) // 2 of a, b, c, d; byte half c // 8
+    byte = word + ((c % 8) // 2) * 16 + (c // 8) * 2 + c % 2
+    r = np.arange(n, dtype=np.int64)
+    scale = (r // 32) * 32 + (r % 8) * 4 + (r % 32) // 8
+    return byte, scale
+
+
+def unpack_allspark(packed: np.ndarray, packed_scales: np.ndarray, n: int):
+    """unpack_allspark (csrc/allspark_layout.cu:8-35): (INT8 weight [n, k], BF16 scale
+    bits [n]) from packed UINT8 [padded_n, k] and BF16 bits [padded_n]; code = byte ^ 0x80
+    (:20-23)."""
+    k = packed.shape[1]
+    byte, scale = allspark_unpack_index(n, k)
+    weight = (packed.reshape(-1)[byte] ^ np.uint8(0x80)).view(np.int8)
+    return weight, np.asarray(packed_scales)[scale]
+
+
+def pack_allspark(codes_u8: np.ndarray, scale_bits: np.ndarray, fill: int = 0x80):
+    """Forward N32K16 packer: the inverse of unpack_allspark's index map. Biased UINT8
+    codes [n, k] and BF16 scale bits [n] -> (packed [padded_n, k], packed scales
+    [padded_n]); bytes and scales of padding rows are `fill` and 0 (never read)."""
+    n, k = codes_u8.shape
+    padded = allspark_padded_rows(n)
+    packed = np.full(padded * k, fill, dtype=np.uint8)
+    packed_scales = np.zeros(padded, dtype=np.uint16)
+    byte, scale = allspark_unpack_index(n, k)
+    packed[byte] = codes_u8
+    packed_scales[scale] = scale_bits
+    return packed.reshape(padded, k), packed_scales
 
 
 # ---------------------------------------------------------------- weight encoding

@@ -22,6 +22,7 @@ def test_header_declares_the_expected_entry_points():
         "ci8_last_error", "ci8_version", "ci8_quantize_rows", "ci8_quantize_grouped4096",
         "ci8_fused_channel_mm", "ci8_cutlass_channel_mm", "ci8_channel_mm",
         "ci8_channel_gemv", "ci8_grouped_summed_mm", "ci8_silu_mul", "ci8_silu_mul_quantize",
+        "ci8_unpack_allspark",
     ])
 
 
@@ -149,6 +150,26 @@ def test_swiglu_rejections(lib):
            A.CI8_ERR_OVERLAP, "must not overlap")
 
 
+def test_unpack_allspark_rejections_cpu(lib):
+    """csrc/bindings.cpp:276-284: N % 16, K % 16, K <= 65536, the INT_MAX bound on the
+    padded buffer, 4-byte packed and 16-byte weight alignment."""
+    from consumer_int8 import _abi as A
+
+    for n, k in [(0, 16), (24, 16), (16, 0), (16, 24), (16, 65552), (1 << 16, 1 << 16)]:
+        status = lib.ci8_unpack_allspark(FAKE, FAKE, FAKE, FAKE, n, k, None)
+        assert status in (A.CI8_ERR_GEOMETRY, A.CI8_ERR_TOO_LARGE)
+    expect(lib, lib.ci8_unpack_allspark(FAKE, FAKE, FAKE, FAKE, 1 << 16, 1 << 16, None),
+           A.CI8_ERR_TOO_LARGE, "Weight too large")
+    expect(lib, lib.ci8_unpack_allspark(FAKE, FAKE, FAKE, FAKE, 24, 16, None),
+           A.CI8_ERR_GEOMETRY, "Expected AllSpark N32K16 weights and channel scales")
+    expect(lib, lib.ci8_unpack_allspark(FAKE + 2, FAKE, FAKE << 4, FAKE << 5, 16, 16, None),
+           A.CI8_ERR_ALIGNMENT, "Unaligned weights")
+    expect(lib, lib.ci8_unpack_allspark(FAKE, FAKE << 6, (FAKE << 4) + 8, FAKE << 5, 16, 16, None),
+           A.CI8_ERR_ALIGNMENT, "Unaligned weights")
+    expect(lib, lib.ci8_unpack_allspark(FAKE, FAKE << 6, FAKE + 256, FAKE << 5, 16, 16, None),
+           A.CI8_ERR_OVERLAP, "must not overlap")
+
+
 def test_torch_surface_matches_reference_schemas():
     import torch
 
@@ -165,6 +186,7 @@ def test_torch_surface_matches_reference_schemas():
         "grouped_summed_mm": "(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) out) -> ()",
         "silu_mul": "(Tensor input, Tensor(a!) out) -> ()",
         "silu_mul_quantize": "(Tensor input, Tensor(a!) codes, Tensor(b!) scales) -> ()",
+        "unpack_allspark": "(Tensor packed, Tensor packed_scales, Tensor(a!) weight, Tensor(b!) scales) -> ()",
     }
     for name, schema in expected.items():
         handle = getattr(ops, name)
@@ -202,3 +224,7 @@ def test_fake_tensor_registration():
         codes = torch.empty(2, 8704, dtype=torch.int8)
         assert ops.silu_mul(x, act) is None
         assert ops.silu_mul_quantize(x, codes, torch.empty(2)) is None
+        packed = torch.empty(32, 16, dtype=torch.uint8)
+        assert ops.unpack_allspark(packed, torch.empty(32, dtype=torch.bfloat16),
+                                   torch.empty(16, 16, dtype=torch.int8),
+                                   torch.empty(16, dtype=torch.bfloat16)) is None

@@ -395,3 +395,79 @@ def test_silu_mul_quantize_is_quantize_rows_of_the_activations():
         for t in rng.choice(8704, 40, replace=False):
             q = E.rne_int(E.f32(Fraction(float(act[r - 1, t])) / s))
             assert int(codes[r, t]) == max(-127, min(127, q))
+
+
+# ------------------------------------------------------------------ AllSpark N32K16
+
+def reference_unpack_loops(packed, packed_scales, n, k):
+    """The reference kernel's word operations (csrc/allspark_layout.cu:10-26) one vector
+    at a time on little-endian uint32 words: an independent restatement of the oracle's
+    vectorised index map."""
+    words = packed.reshape(-1).view("<u4")
+    weight = np.zeros((n, k), np.uint8)
+    scales = np.zeros(n, np.uint16)
+    for vector in range(n * (k // 16)):
+        row, tile = divmod(vector, k // 16)
+        packed_row = (row // 32) * 8 + row % 8
+        offset = packed_row * k * 4 + tile * 64 + ((row % 32) // 16) * 8 + ((row % 16) // 8) * 4
+        a, b, c, d = (int(words[offset // 4 + 4 * j]) for j in range(4))
+        out = [((a & 0xFFFF) | (b << 16)) & 0xFFFFFFFF, ((c & 0xFFFF) | (d << 16)) & 0xFFFFFFFF,
+               (a >> 16) | (b & 0xFFFF0000), (c >> 16) | (d & 0xFFFF0000)]
+        piece = np.array([w ^ 0x80808080 for w in out], "<u4").view(np.uint8)
+        weight[row, tile * 16:(tile + 1) * 16] = piece
+        if tile == 0:
+            scales[row] = packed_scales[(row // 32) * 32 + (row % 8) * 4 + (row % 32) // 8]
+    return weight.view(np.int8), scales
+
+
+@pytest.mark.parametrize("n,k", [(16, 16), (48, 80), (64, 32), (128, 512)])
+def test_allspark_unpack_matches_the_reference_word_operations(n, k):
+    rng = np.random.default_rng(319 + n + k)
+    padded = O.allspark_padded_rows(n)
+    packed = rng.integers(0, 256, (padded, k)).astype(np.uint8)
+    packed_scales = rng.integers(0, 1 << 16, padded).astype(np.uint16)
+    w, s = O.unpack_allspark(packed, packed_scales, n)
+    rw, rs = reference_unpack_loops(packed, packed_scales, n, k)
+    assert np.array_equal(w, rw) and np.array_equal(s, rs)
+
+
+@pytest.mark.parametrize("n,k", [(16, 16), (48, 80), (128, 512), (5120, 3072)])
+def test_allspark_pack_is_the_inverse_and_padding_is_never_read(n, k):
+    """tests/test_cuda_ops.py:440-471's shapes: unpack(pack(codes)) == codes - 128 and the
+    scales, the index map is a bijection onto the valid bytes, and the padding bytes can
+    hold anything."""
+    rng = np.random.default_rng(319)
+    codes = rng.integers(0, 256, (n, k)).astype(np.uint8)
+    scales = rng.integers(0, 1 << 16, n).astype(np.uint16)
+    byte, sidx = O.allspark_unpack_index(n, k)
+    assert np.unique(byte).size == n * k and np.unique(sidx).size == n
+    assert byte.max() < O.allspark_padded_rows(n) * k
+    for fill in (0x80, 0x00, 0xFF):
+        packed, packed_scales = O.pack_allspark(codes, scales, fill=fill)
+        assert packed.shape == (O.allspark_padded_rows(n), k)
+        w, s = O.unpack_allspark(packed, packed_scales, n)
+        assert np.array_equal(w, (codes.astype(np.int16) - 128).astype(np.int8))
+        assert np.array_equal(s, scales)
+
+
+def test_allspark_known_layout():
+    """Hand-read N32K16 placement: packed row 0, tile 0 holds rows 0, 8, 16, 24 for
+    k = 0..15; its first 16 bytes are, per row, the codes of k = 0, 1, 8, 9, and its
+    second 16 bytes those of k = 2, 3, 10, 11. Packed row 1 holds rows 1, 9, 17, 25;
+    scales of rows 0, 8, 16, 24, 1 sit at packed positions 0, 1, 2, 3, 4."""
+    n, k = 32, 32
+    codes = np.zeros((n, k), np.uint8)
+    for r in range(n):
+        for c in range(k):
+            codes[r, c] = (r * 5 + c * 3) % 256
+    scales = np.arange(100, 100 + n, dtype=np.uint16)
+    packed, packed_scales = O.pack_allspark(codes, scales)
+    flat = packed.reshape(-1)
+    expect0 = [codes[r, c] for r in (0, 8, 16, 24) for c in (0, 1, 8, 9)]
+    expect1 = [codes[r, c] for r in (0, 8, 16, 24) for c in (2, 3, 10, 11)]
+    assert flat[:16].tolist() == expect0
+    assert flat[16:32].tolist() == expect1
+    # tile 1 of packed row 0 (k = 16..31) follows at byte 64; packed row 1 at 4k = 128
+    assert flat[64:68].tolist() == [codes[0, c] for c in (16, 17, 24, 25)]
+    assert flat[128:132].tolist() == [codes[1, c] for c in (0, 1, 8, 9)]
+    assert packed_scales[:5].tolist() == [100, 108, 116, 124, 101]
