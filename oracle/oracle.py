@@ -374,6 +374,35 @@ def quantize_channel(weight: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     return (codes.astype(np.int16) + 128).astype(np.uint8), stored
 
 
+def quantize_group32(weight: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """[N, K] float -> (INT8 codes [N, K], FP32 scales [N, ceil(K/32)]).
+
+    src/consumer_int8/quantization.py:35-47: blocks of 32 input channels, the last one
+    zero-padded (:38); scale = amax_block / 127 in FP32, 1 where that is 0 (:39-40);
+    codes = clamp(rne(w / scale), -127, 127) (:41). Rejects non-finite weights (:17-18).
+    """
+    value = np.asarray(weight, dtype=np.float32)
+    if value.ndim != 2 or value.size == 0:
+        raise ValueError("Expected a nonempty floating-point weight matrix")
+    if not np.isfinite(value).all():
+        raise ValueError("Weight contains non-finite values")
+    n, k = value.shape
+    blocks = -(-k // 32)
+    padded = np.zeros((n, blocks * 32), np.float32)
+    padded[:, :k] = value
+    padded = padded.reshape(n, blocks, 32)
+    scale = (np.abs(padded).max(axis=2) / np.float32(127.0)).astype(np.float32)
+    scale = np.where(scale > 0, scale, np.float32(1.0)).astype(np.float32)
+    codes = np.clip(np.rint((padded / scale[:, :, None]).astype(np.float32)), -127, 127)
+    return codes.astype(np.int8).reshape(n, blocks * 32)[:, :k].copy(), scale
+
+
+def dequantize_group32(codes: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """codes * scale of each 32-channel block in FP32 (src/consumer_int8/quantization.py:50-51)."""
+    k = codes.shape[1]
+    return (codes.astype(np.float32) * np.repeat(scale, 32, axis=1)[:, :k]).astype(np.float32)
+
+
 def dequantize_channel(codes_u8: np.ndarray, scale_bits: np.ndarray) -> np.ndarray:
     """(codes - 128) * scale in FP32 (src/consumer_int8/quantization.py:46-47)."""
     return ((np.asarray(codes_u8).astype(np.float32) - np.float32(128))

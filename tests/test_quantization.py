@@ -52,7 +52,40 @@ def test_quantize_channel_rejections():
         quantize_channel(torch.tensor([[1.0, float("inf")]]))
 
 
+def scale_sensitive_weights():
+    """Rows whose maximum A gives fl(A / 127) != fl(A * fl(1 / 127)), filled with values
+    midway between (c + 0.5) times either scale: they round to different codes under the
+    two scales, so only the correctly rounded scale reproduces the oracle's codes.
+    Returns (weights, codes under the reciprocal scale)."""
+    rng = np.random.default_rng(5)
+    amax = (rng.random(20000) * 10 + 0.1).astype(np.float32)
+    ieee = (amax / np.float32(127)).astype(np.float32)
+    recip = (amax * (np.float32(1) / np.float32(127))).astype(np.float32)
+    pick = np.flatnonzero(ieee != recip)[:512]
+    assert pick.size == 512
+    c = np.arange(1, 126, dtype=np.float64) + 0.5
+    mid = (ieee[pick, None].astype(np.float64) + recip[pick, None]) / 2 * c[None, :]
+    w = np.concatenate([amax[pick, None], mid.astype(np.float32)], axis=1)
+    wrong = np.clip(np.rint((w / recip[pick, None]).astype(np.float32)), -128, 127) + 128
+    return w, wrong.astype(np.uint8)
+
+
+def test_scale_sensitive_weights_separate_the_two_scales():
+    w, wrong = scale_sensitive_weights()
+    o_codes, _ = O.quantize_channel(w)
+    assert (wrong != o_codes).sum() > 1000
+
+
 @pytest.mark.gpu
 def test_quantize_channel_on_gpu(ops):
+    """Includes rows where a scale quotient off by one ULP changes the codes: torch's GPU
+    division by a host scalar is a reciprocal multiplication, off in about 5% of rows."""
+    from consumer_int8.quantization import quantize_channel
+
     check_known_answer("cuda")
     check_matches_oracle("cuda")
+    w, _ = scale_sensitive_weights()
+    codes, scale = quantize_channel(torch.from_numpy(w).to("cuda"))
+    o_codes, o_scale = O.quantize_channel(w)
+    assert np.array_equal(codes.cpu().numpy(), o_codes)
+    assert np.array_equal(scale.view(torch.int16).cpu().numpy().view(np.uint16), o_scale)
