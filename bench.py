@@ -335,6 +335,43 @@ def main() -> int:
                                           "frac": round(bu / (mean_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
                                           "mean_us": round(mean_us, 2), "bytes": bu}
         del pk, pks, wu, su
+        # Block-32 Q8_0 W8A8 at the reference harness's largest default shape
+        # (benchmarks/benchmark_q8_block_int8.py:45, :253): M=2048, N=1024, K=4096,
+        # through the C ABI as that harness calls it. The per-block FP32 rescale (3 VALU
+        # instructions per output per block) bounds it, so the VALU fraction is reported
+        # beside the MFMA one.
+        from consumer_int8 import _abi
+
+        lib = _abi.load()
+        MQ, NQ, KQ = 2048, 1024, 4096
+        xq = (torch.randn(MQ, KQ, generator=gen, device="cuda") * 0.1).to(torch.bfloat16)
+        wq = torch.randint(-128, 128, (NQ, KQ), generator=gen, device="cuda", dtype=torch.int8)
+        swq = (torch.randn(NQ, KQ // 32, generator=gen, device="cuda") * 0.01).half()
+        aq = torch.empty(MQ, KQ, device="cuda", dtype=torch.int8)
+        saq = torch.empty(MQ, KQ // 32, device="cuda")
+        yq = torch.empty(MQ, NQ, device="cuda", dtype=torch.bfloat16)
+        qstream = torch.cuda.current_stream().cuda_stream
+        args_q = [t.data_ptr() for t in (xq, aq, saq, wq, swq, yq)]
+
+        def q8_fused():
+            assert lib.ci8_q8_block_int8(*args_q, MQ, NQ, KQ, qstream) == 0
+
+        def q8_mm():
+            assert lib.ci8_q8_block_mm(aq.data_ptr(), saq.data_ptr(), wq.data_ptr(),
+                                       swq.data_ptr(), yq.data_ptr(), MQ, NQ, KQ, qstream) == 0
+
+        q8_fused()
+        ops_q = 2 * MQ * NQ * KQ
+        valu_peak = cus * 64 * 2.4e9  # lane-instructions per second, 64 lanes/clk/CU
+        for name, call in (("q8_block_int8", q8_fused), ("q8_block_mm", q8_mm)):
+            mean_us, _ = time_kernel(torch, [call], 8)
+            tops = ops_q / (mean_us * 1e-6) / 1e12
+            rescale = 3 * MQ * NQ * (KQ // 32) / (mean_us * 1e-6)
+            extras[name] = {"bound": "valu", "achieved": round(tops, 1), "peak": round(peak_tops, 1),
+                            "unit": "TFLOP/s", "frac": round(tops / peak_tops, 4),
+                            "valu_frac": round(rescale / valu_peak, 4),
+                            "mean_us": round(mean_us, 2), "ops": ops_q}
+        del xq, wq, swq, aq, saq, yq
         # quantize_rows + fused_channel_mm at M=128, K=4096, N=4096; AI 234
         # op/B is below the ridge, so this small case is bounded by HBM (bytes below).
         M1, K1, N1 = 128, 4096, 4096

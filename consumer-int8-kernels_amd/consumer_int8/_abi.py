@@ -35,6 +35,9 @@ SIGNATURES = {
     "ci8_silu_mul": ([_p, _p, _i64, _i64, _p], ctypes.c_int),
     "ci8_silu_mul_quantize": ([_p, _p, _p, _i64, _i64, _p], ctypes.c_int),
     "ci8_unpack_allspark": ([_p, _p, _p, _p, _i64, _i64, _p], ctypes.c_int),
+    "ci8_quantize_block32": ([_p, _p, _p, _i64, _i64, _p], ctypes.c_int),
+    "ci8_q8_block_mm": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p], ctypes.c_int),
+    "ci8_q8_block_int8": ([_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p], ctypes.c_int),
 }
 
 _lib = None

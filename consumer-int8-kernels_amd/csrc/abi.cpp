@@ -53,6 +53,15 @@ int check_gemm(int64_t m, int64_t n, int64_t k, bool need_n4, const char* what) 
   return CI8_OK;
 }
 
+// benchmarks/cuda/q8_block_int8.cu:142-174: m, n, k > 0 and k % 32 == 0.
+int check_q8(int64_t m, int64_t n, int64_t k) {
+  if (!(m > 0 && n > 0 && k > 0 && k % 32 == 0))
+    return fail(CI8_ERR_GEOMETRY, "Invalid block-32 geometry");
+  if (m * k > INT_MAX || n * k > INT_MAX || m * n > INT_MAX)
+    return fail(CI8_ERR_TOO_LARGE, "Matrix too large");
+  return CI8_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -198,6 +207,47 @@ int ci8_unpack_allspark(const uint8_t* packed, const void* packed_scales, int8_t
     return fail(CI8_ERR_OVERLAP, "AllSpark buffers must not overlap");
   return launched(ci8::launch_unpack_allspark(packed, packed_scales, weight, scales, int(n),
                                               int(k), as_stream(stream)));
+}
+
+int ci8_quantize_block32(const void* x, int8_t* a, float* sa, int64_t m, int64_t k,
+                         void* stream) {
+  if (int status = check_q8(m, 1, k)) return status;
+  if (!aligned(x, 2) || !aligned(sa, 4))
+    return fail(CI8_ERR_ALIGNMENT, "Block-32 quantization requires aligned buffers");
+  if (overlap(x, m * k * 2, a, m * k) || overlap(x, m * k * 2, sa, m * k / 8) ||
+      overlap(a, m * k, sa, m * k / 8))
+    return fail(CI8_ERR_OVERLAP, "Block-32 buffers must not overlap");
+  return launched(ci8::launch_quantize_block32(x, a, sa, int(m), int(k), as_stream(stream)));
+}
+
+int ci8_q8_block_mm(const int8_t* a, const float* sa, const int8_t* w, const void* sw, void* y,
+                    int64_t m, int64_t n, int64_t k, void* stream) {
+  if (int status = check_q8(m, n, k)) return status;
+  if (!aligned(a, 16) || !aligned(w, 16) || !aligned(sa, 4) || !aligned(sw, 2) ||
+      !aligned(y, 2))
+    return fail(CI8_ERR_ALIGNMENT, "Block-32 GEMM requires aligned buffers");
+  if (overlap(y, m * n * 2, a, m * k) || overlap(y, m * n * 2, w, n * k) ||
+      overlap(y, m * n * 2, sa, m * k / 8) || overlap(y, m * n * 2, sw, n * k / 16))
+    return fail(CI8_ERR_OVERLAP, "Block-32 buffers must not overlap");
+  return launched(
+      ci8::launch_q8_block_mm(a, sa, w, sw, y, int(m), int(n), int(k), as_stream(stream)));
+}
+
+int ci8_q8_block_int8(const void* x, int8_t* a, float* sa, const int8_t* w, const void* sw,
+                      void* y, int64_t m, int64_t n, int64_t k, void* stream) {
+  if (int status = check_q8(m, n, k)) return status;
+  if (!aligned(x, 2) || !aligned(a, 16) || !aligned(w, 16) || !aligned(sa, 4) ||
+      !aligned(sw, 2) || !aligned(y, 2))
+    return fail(CI8_ERR_ALIGNMENT, "Block-32 GEMM requires aligned buffers");
+  if (overlap(x, m * k * 2, a, m * k) || overlap(x, m * k * 2, sa, m * k / 8) ||
+      overlap(a, m * k, sa, m * k / 8) || overlap(y, m * n * 2, x, m * k * 2) ||
+      overlap(y, m * n * 2, a, m * k) || overlap(y, m * n * 2, w, n * k) ||
+      overlap(y, m * n * 2, sa, m * k / 8) || overlap(y, m * n * 2, sw, n * k / 16))
+    return fail(CI8_ERR_OVERLAP, "Block-32 buffers must not overlap");
+  const hipStream_t s = as_stream(stream);
+  const hipError_t q = ci8::launch_quantize_block32(x, a, sa, int(m), int(k), s);
+  if (q != hipSuccess) return launched(q);
+  return launched(ci8::launch_q8_block_mm(a, sa, w, sw, y, int(m), int(n), int(k), s));
 }
 
 }  // extern "C"

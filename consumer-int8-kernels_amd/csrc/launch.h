@@ -40,6 +40,15 @@ hipError_t launch_unpack_allspark(const uint8_t* packed, const void* packed_scal
                                   int8_t* weight, void* scales, int n, int k,
                                   hipStream_t stream);
 
+// x BF16 [m, k] -> a INT8 [m, k], sa FP32 [m, k/32] (per 32 values as quantize_rows).
+hipError_t launch_quantize_block32(const void* x, int8_t* a, float* sa, int m, int k,
+                                   hipStream_t stream);
+// y BF16 [m, n] from block-32 W8A8: a INT8 [m, k], sa FP32 [m, k/32], w INT8 [n, k],
+// sw FP16 [n, k/32]. Requires k % 32 == 0, a and w 16-byte aligned.
+hipError_t launch_q8_block_mm(const int8_t* a, const float* sa, const int8_t* w,
+                              const void* sw, void* y, int m, int n, int k,
+                              hipStream_t stream);
+
 hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale, void* out,
                                int m, int n, int k, hipStream_t stream);
 

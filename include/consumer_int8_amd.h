@@ -23,6 +23,10 @@
  *   ci8_silu_mul_quantize    csrc/silu_quant.h:6-7, csrc/bindings.cpp:46-64, schema :595
  *   ci8_unpack_allspark      csrc/kernels.h:52-53, csrc/bindings.cpp:266-288,
  *                            schema :607
+ *   ci8_q8_block_int8        benchmarks/cuda/q8_block_int8.cu:142-152 (q8_block_int8 and
+ *                            its tiled variants :154-174, same contract)
+ *   ci8_quantize_block32,    its two stages, benchmarks/cuda/q8_block_int8.cu:11-23 and
+ *   ci8_q8_block_mm          :25-63, as separate entry points
  */
 #ifndef CONSUMER_INT8_AMD_H
 #define CONSUMER_INT8_AMD_H
@@ -154,6 +158,31 @@ int ci8_silu_mul_quantize(const void* x, int8_t* codes, float* scales, int64_t m
  *           csrc/bindings.cpp:276-284. */
 int ci8_unpack_allspark(const uint8_t* packed, const void* packed_scales, int8_t* weight,
                         void* scales, int64_t n, int64_t k, void* stream);
+
+/* quantize_block32: x BF16 [m,k] -> a INT8 [m,k] and sa FP32 [m,k/32]; every run of
+ * 32 consecutive values is quantized as ci8_quantize_rows quantizes a row. Requires
+ * m, k > 0, k % 32 == 0, m*k <= INT_MAX, no overlap; x 2-byte, sa 4-byte aligned.
+ * Replaces: the quantize kernel of benchmarks/cuda/q8_block_int8.cu:11-23. */
+int ci8_quantize_block32(const void* x, int8_t* a, float* sa, int64_t m, int64_t k,
+                         void* stream);
+
+/* q8_block_mm: block-32 W8A8 (GGUF Q8_0 weights with activations quantized per 32):
+ * a INT8 [m,k], sa FP32 [m,k/32], w INT8 [n,k] (signed codes), sw FP16 [n,k/32]
+ * -> y BF16 [m,n] = bf16_rn(sum), sum over blocks b ascending from +0 of
+ * fma(float(acc_b), fl(sa[m,b] * float(sw[n,b])), sum), acc_b the exact INT32 dot
+ * product of block b. Requires m, n, k > 0, k % 32 == 0, each of m*k, n*k, m*n <=
+ * INT_MAX, a and w 16-byte aligned, y not overlapping an input.
+ * Replaces: the matmul kernel of benchmarks/cuda/q8_block_int8.cu:25-63. */
+int ci8_q8_block_mm(const int8_t* a, const float* sa, const int8_t* w, const void* sw, void* y,
+                    int64_t m, int64_t n, int64_t k, void* stream);
+
+/* q8_block_int8: ci8_quantize_block32 then ci8_q8_block_mm on the caller's a and sa
+ * (scratch the caller owns, as in the reference).
+ * Replaces: extern "C" int q8_block_int8(const void* x, void* a, float* sa,
+ *           const void* w, const void* sw, void* y, int m, int n, int k, cudaStream_t),
+ *           benchmarks/cuda/q8_block_int8.cu:142-152. */
+int ci8_q8_block_int8(const void* x, int8_t* a, float* sa, const int8_t* w, const void* sw,
+                      void* y, int64_t m, int64_t n, int64_t k, void* stream);
 
 #ifdef __cplusplus
 }

@@ -2,8 +2,9 @@
 
 This module restates, in numpy, the arithmetic of AppMana/consumer-int8-kernels for
 quantize_rows, quantize_grouped4096, fused/cutlass_channel_mm, channel_mm, channel_gemv,
-the channel weight encoding, the SwiGLU producers silu_mul / silu_mul_quantize and the
-AllSpark N32K16 weight layout (unpack_allspark, with its inverse packer). Only tests/, __graft_entry__.smoke() and bench.py's
+the channel weight encoding, the SwiGLU producers silu_mul / silu_mul_quantize, the
+AllSpark N32K16 weight layout (unpack_allspark, with its inverse packer) and the
+block-32 Q8_0 W8A8 path (quantize_block32, q8_block_mm). Only tests/, __graft_entry__.smoke() and bench.py's
 cpu_baseline leg may import it, and only as the checker (or the timed CPU baseline);
 the product path never calls it and has no CPU fallback.
 
@@ -293,6 +294,77 @@ def bf16_ulp(values: np.ndarray) -> np.ndarray:
     exp = np.floor(np.log2(np.where(v > 0, v, 2.0**-126)))
     exp = np.maximum(exp, -126)
     return 2.0 ** (exp - 7)
+
+
+# ---------------------------------------------------------------- block-32 Q8_0 W8A8
+
+def fma_f32(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
+    """fl32(a * b + c) with a single rounding, for float32 inputs (finite results).
+
+    a * b is exact in float64 (48 significant bits); the float64 sum s = fl64(p + c)
+    and its exact error e (Knuth's TwoSum) carry a + b*c exactly. Rounding s to float32
+    is the correct result unless s is exactly halfway between two float32 values, in
+    which case e (if nonzero) decides the side.
+    """
+    p = np.asarray(a, np.float64) * np.asarray(b, np.float64)
+    c = np.asarray(c, np.float64)
+    s = p + c
+    bp = s - p
+    e = (p - (s - bp)) + (c - bp)
+    r = s.astype(np.float32)
+    up = np.nextafter(r, np.float32(np.inf))
+    down = np.nextafter(r, np.float32(-np.inf))
+    mid_up = (r.astype(np.float64) + up) / 2
+    mid_down = (r.astype(np.float64) + down) / 2
+    r = np.where((s == mid_up) & (e > 0), up, r)
+    r = np.where((s == mid_down) & (e < 0), down, r)
+    return r.astype(np.float32)
+
+
+def f16_to_f32(bits: np.ndarray) -> np.ndarray:
+    """IEEE binary16 bit patterns (uint16) -> float32, exactly."""
+    return np.asarray(bits, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def quantize_block32(x_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """BF16 [M, K] -> (INT8 codes [M, K], FP32 scales [M, K/32]).
+
+    benchmarks/cuda/q8_block_int8.cu:11-23: per run of 32 consecutive values, amax by
+    fmaxf from |v| (:16-18), s = fmaxf(amax / 127, 1e-20) (:19), code =
+    __float2int_rn(v / s) (:20) -- quantize_rows' arithmetic on rows of 32.
+    """
+    m, k = x_bits.shape
+    codes, scales = quantize_rows(np.ascontiguousarray(x_bits).reshape(m * k // 32, 32))
+    return codes.reshape(m, k), scales.reshape(m, k // 32)
+
+
+def q8_block_mm(a: np.ndarray, sa: np.ndarray, w: np.ndarray, sw_bits: np.ndarray) -> np.ndarray:
+    """Block-32 W8A8 GEMM: BF16 bits [M, N].
+
+    benchmarks/cuda/q8_block_int8.cu:25-63: for each block b of 32 K values in ascending
+    order, acc_b = exact INT32 dot product (:43-46), then
+    sum = fma(float(acc_b), fl(sa[m, b] * float(sw[n, b])), sum) (:52-53, the product
+    and add contracted as the CUDA compiler does), sum from 0; out = bf16_rn(sum) (:61).
+    sw holds FP16 bit patterns.
+    """
+    m, k = a.shape
+    n = w.shape[0]
+    total = np.zeros((m, n), np.float32)
+    sw = f16_to_f32(sw_bits)
+    for b in range(k // 32):
+        cols = slice(32 * b, 32 * b + 32)
+        acc = (a[:, cols].astype(np.float64) @ w[:, cols].astype(np.float64).T).astype(np.float32)
+        scale = (sa[:, b, None].astype(np.float32) * sw[None, :, b]).astype(np.float32)
+        total = fma_f32(acc, scale, total)
+    return f32_to_bf16(total)
+
+
+def q8_block_dense_reference(x_bits: np.ndarray, w: np.ndarray, sw_bits: np.ndarray) -> np.ndarray:
+    """float64 x @ (w * sw)^T, the unquantized product the reference benchmark compares
+    against (benchmarks/benchmark_q8_block_int8.py:112-115)."""
+    n, k = w.shape
+    dense = w.astype(np.float64).reshape(n, k // 32, 32) * f16_to_f32(sw_bits)[..., None]
+    return bf16_to_f32(x_bits).astype(np.float64) @ dense.reshape(n, k).T
 
 
 # ---------------------------------------------------------------- AllSpark N32K16

@@ -22,7 +22,7 @@ def test_header_declares_the_expected_entry_points():
         "ci8_last_error", "ci8_version", "ci8_quantize_rows", "ci8_quantize_grouped4096",
         "ci8_fused_channel_mm", "ci8_cutlass_channel_mm", "ci8_channel_mm",
         "ci8_channel_gemv", "ci8_grouped_summed_mm", "ci8_silu_mul", "ci8_silu_mul_quantize",
-        "ci8_unpack_allspark",
+        "ci8_unpack_allspark", "ci8_quantize_block32", "ci8_q8_block_mm", "ci8_q8_block_int8",
     ])
 
 
@@ -167,6 +167,33 @@ def test_unpack_allspark_rejections_cpu(lib):
     expect(lib, lib.ci8_unpack_allspark(FAKE, FAKE << 6, (FAKE << 4) + 8, FAKE << 5, 16, 16, None),
            A.CI8_ERR_ALIGNMENT, "Unaligned weights")
     expect(lib, lib.ci8_unpack_allspark(FAKE, FAKE << 6, FAKE + 256, FAKE << 5, 16, 16, None),
+           A.CI8_ERR_OVERLAP, "must not overlap")
+
+
+def test_q8_block_rejections(lib):
+    """benchmarks/cuda/q8_block_int8.cu:145-146: m, n, k > 0 and k % 32 == 0; plus the
+    INT_MAX bound, alignment and overlap."""
+    from consumer_int8 import _abi as A
+
+    for m, n, k in [(0, 4, 32), (4, 0, 32), (4, 4, 0), (4, 4, 48), (-1, 4, 32)]:
+        expect(lib, lib.ci8_q8_block_int8(FAKE, FAKE << 1, FAKE << 2, FAKE << 3, FAKE << 4,
+                                          FAKE << 5, m, n, k, None),
+               A.CI8_ERR_GEOMETRY, "Invalid block-32 geometry")
+        expect(lib, lib.ci8_q8_block_mm(FAKE, FAKE << 1, FAKE << 2, FAKE << 3, FAKE << 4,
+                                        m, n, k, None),
+               A.CI8_ERR_GEOMETRY, "Invalid block-32 geometry")
+    expect(lib, lib.ci8_quantize_block32(FAKE, FAKE << 1, FAKE << 2, 4, 48, None),
+           A.CI8_ERR_GEOMETRY, "Invalid block-32 geometry")
+    expect(lib, lib.ci8_q8_block_mm(FAKE, FAKE << 1, FAKE << 2, FAKE << 3, FAKE << 4,
+                                    1 << 16, 4, 1 << 16, None),
+           A.CI8_ERR_TOO_LARGE, "Matrix too large")
+    expect(lib, lib.ci8_q8_block_mm(FAKE + 8, FAKE << 1, FAKE << 2, FAKE << 3, FAKE << 4,
+                                    4, 4, 32, None),
+           A.CI8_ERR_ALIGNMENT, "aligned buffers")
+    expect(lib, lib.ci8_q8_block_mm(FAKE, FAKE << 1, FAKE << 2, FAKE << 3, FAKE + 64,
+                                    4, 4, 32, None),
+           A.CI8_ERR_OVERLAP, "must not overlap")
+    expect(lib, lib.ci8_quantize_block32(FAKE, FAKE + 64, FAKE << 2, 4, 32, None),
            A.CI8_ERR_OVERLAP, "must not overlap")
 
 

@@ -471,3 +471,88 @@ def test_allspark_known_layout():
     assert flat[64:68].tolist() == [codes[0, c] for c in (16, 17, 24, 25)]
     assert flat[128:132].tolist() == [codes[1, c] for c in (0, 1, 8, 9)]
     assert packed_scales[:5].tolist() == [100, 108, 116, 124, 101]
+
+
+# ------------------------------------------------------------------ block-32 Q8_0
+
+def test_fma_f32_matches_exact_single_rounding():
+    """Random operands and constructed halfway cases (a*b + c exactly between two
+    float32 values, then nudged by a tiny c) against exact rationals."""
+    rng = np.random.default_rng(61)
+    a = (rng.standard_normal(3000) * 10.0 ** rng.integers(-8, 8, 3000)).astype(np.float32)
+    b = (rng.standard_normal(3000) * 10.0 ** rng.integers(-8, 8, 3000)).astype(np.float32)
+    c = (rng.standard_normal(3000) * 10.0 ** rng.integers(-12, 12, 3000)).astype(np.float32)
+    # halfway constructions: (1 + i 2^-12)(1 + j 2^-12) with i, j odd has 25 significant
+    # bits, so it lies exactly halfway between two float32 values; c = 0 ties to even,
+    # c = +/- 2^-60 decides the side.
+    i = rng.integers(0, 512, 300) * 2 + 1
+    j = rng.integers(0, 512, 300) * 2 + 1
+    ha = (1 + i * 2.0**-12).astype(np.float32)
+    hb = (1 + j * 2.0**-12).astype(np.float32)
+    assert all(E.f32(Fraction(float(p)) * Fraction(float(q))) != Fraction(float(p)) * Fraction(float(q))
+               for p, q in zip(ha[:20], hb[:20]))
+    tiny = np.float32(2.0**-60)
+    a = np.concatenate([a, ha, ha, ha]).astype(np.float32)
+    b = np.concatenate([b, hb, hb, hb]).astype(np.float32)
+    c = np.concatenate([c, np.zeros(300, np.float32), np.full(300, tiny), np.full(300, -tiny)])
+    plain = (a.astype(np.float64) * b + c).astype(np.float32)  # double rounding
+    assert np.sum(plain != O.fma_f32(a, b, c)) > 100         # the cases that matter
+    got = O.fma_f32(a, b, c)
+    for x, y, z, g in zip(a, b, c, got):
+        exact = Fraction(float(x)) * Fraction(float(y)) + Fraction(float(z))
+        want = E.f32(exact)
+        assert float(want) == float(g), (x, y, z, g, float(want))
+
+
+def test_quantize_block32_is_quantize_rows_per_block():
+    """benchmarks/cuda/q8_block_int8.cu:11-23: a zero block gets 1e-20, a x100 block is
+    scaled on its own, and each block matches quantize_rows of those 32 values."""
+    rng = np.random.default_rng(62)
+    x = (rng.standard_normal((5, 96)) * 0.1).astype(np.float32)
+    x[:, :32] = 0
+    x[:, 32:64] *= 100
+    bits = O.f32_to_bf16(x)
+    codes, scales = O.quantize_block32(bits)
+    assert scales.shape == (5, 3) and codes.shape == (5, 96)
+    assert np.all(scales[:, 0] == np.float32(1e-20)) and not codes[:, :32].any()
+    for r in range(5):
+        for blk in range(3):
+            c, s = O.quantize_rows(bits[r:r + 1, 32 * blk:32 * blk + 32])
+            assert np.array_equal(codes[r:r + 1, 32 * blk:32 * blk + 32], c)
+            assert scales[r, blk] == s[0]
+
+
+def test_q8_block_mm_matches_exact_rationals_and_the_reference_tolerance():
+    """The oracle's GEMM against a Fraction evaluation of the same rounding sequence on
+    a tiny case, and against the reference benchmark's own checks
+    (benchmarks/benchmark_q8_block_int8.py:90-121): the blockwise dot-product oracle
+    within rtol 0.008 / atol 1e-5 and the dense product within 1.5% relative."""
+    rng = np.random.default_rng(63)
+    m, n, k = 3, 5, 96
+    x = (rng.standard_normal((m, k)) * 0.1).astype(np.float32)
+    x[:, 32:64] *= 100
+    bits = O.f32_to_bf16(x)
+    a, sa = O.quantize_block32(bits)
+    w = rng.integers(-128, 128, (n, k)).astype(np.int8)
+    sw = (rng.standard_normal((n, k // 32)) * 0.01).astype(np.float16).view(np.uint16)
+    y = O.q8_block_mm(a, sa, w, sw)
+    swf = O.f16_to_f32(sw)
+    for r in range(m):
+        for c in range(n):
+            total = Fraction(0)
+            for blk in range(k // 32):
+                acc = int(np.dot(a[r, 32 * blk:32 * blk + 32].astype(np.int64),
+                                 w[c, 32 * blk:32 * blk + 32].astype(np.int64)))
+                scale = E.f32(Fraction(float(sa[r, blk])) * Fraction(float(swf[c, blk])))
+                total = E.f32(Fraction(acc) * scale + total)
+            assert int(y[r, c]) == E.bf16_bits(float(E.bf16(total)))
+    # the reference benchmark's checks
+    blockwise = np.zeros((m, n))
+    for blk in range(k // 32):
+        dot = a[:, 32 * blk:32 * blk + 32].astype(np.float64) @ w[:, 32 * blk:32 * blk + 32].astype(np.float64).T
+        blockwise += dot * (sa[:, blk, None] * swf[None, :, blk])
+    got = O.bf16_to_f32(y).astype(np.float64)
+    ref_bf16 = O.bf16_to_f32(O.f64_to_bf16(blockwise)).astype(np.float64)
+    assert np.all(np.abs(got - ref_bf16) <= 1e-5 + 0.008 * np.abs(ref_bf16))
+    dense = O.q8_block_dense_reference(bits, w, sw)
+    assert np.linalg.norm(got - dense) / np.linalg.norm(dense) < 0.015
