@@ -28,6 +28,56 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
 }
 
+// Low and high BF16 halves of a packed pair, widened to FP32 (exact).
+__device__ __forceinline__ float bf16_lo(uint32_t word) { return __uint_as_float(word << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t word) {
+  return __uint_as_float(word & 0xFFFF0000u);
+}
+
+// rne(q) for |q| <= 127.5 as the low byte of fl(q + 1.5 * 2^23), the two's-complement
+// INT8 code; a NaN q gives 0.
+__device__ __forceinline__ uint32_t code_byte(float q) {
+  return __float_as_uint(q + 12582912.0f) & 0xFFu;
+}
+
+// INT8 codes of eight BF16 values (four packed pairs) for a scale of the row or block they
+// belong to: code = rne(fl(v / scale)), the IEEE quotient, as two words of four bytes.
+// The quotient comes from q0 = fl(v * inv), inv = fl(1 / scale). For every finite v of
+// the row, |v / scale| < 128 (scale >= amax / 127 rounded, or the 1e-20 floor), so
+// |q0 - v/scale| <= 2^-17 + 2^-17 and |fl(v/scale) - v/scale| <= 2^-17: when q0 is more
+// than 2^-15 from every half-integer, fl(v / scale) lies on the same side of each and
+// rounds to the same integer. Lanes holding a value inside that band (about 1 in 16000)
+// take the division. NaN and infinite products give NaN, whose code is 0 as with the
+// division.
+__device__ __forceinline__ u32x2 codes8(const u32x4& packed, float scale, float inv) {
+#pragma clang fp contract(off)
+  float q[8];
+  bool near = false;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    q[2 * j] = bf16_lo(packed[j]) * inv;
+    q[2 * j + 1] = bf16_hi(packed[j]) * inv;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) near |= fabsf(q[j] - __builtin_floorf(q[j]) - 0.5f) <= 0x1p-15f;
+  if (near) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      q[2 * j] = bf16_lo(packed[j]) / scale;
+      q[2 * j + 1] = bf16_hi(packed[j]) / scale;
+    }
+  }
+  u32x2 out;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint32_t bytes = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bytes |= code_byte(q[4 * h + j]) << (8 * j);
+    out[h] = bytes;
+  }
+  return out;
+}
+
 // Raw buffer resource over `bytes` bytes starting at `base`. Loads at byte offsets
 // >= bytes return zero, which covers row and column tails without branches.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {

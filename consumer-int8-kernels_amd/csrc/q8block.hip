@@ -37,10 +37,6 @@ typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------ quantizer
 
-__device__ __forceinline__ uint32_t code_byte(float q) {
-  return __float_as_uint(q + 12582912.0f) & 0xFFu;  // rne(q) for |q| <= 127.5; NaN -> 0
-}
-
 // Four lanes per block, eight values per lane. Requires x 16-byte, a 8-byte aligned.
 __global__ void __launch_bounds__(256) quantize_block32_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ a, float* __restrict__ sa,
@@ -60,16 +56,7 @@ __global__ void __launch_bounds__(256) quantize_block32_kernel(
   if (!live) return;
   const float scale = fmaxf(amax / 127.f, 1e-20f);
   if ((threadIdx.x & 3) == 0) sa[block] = scale;
-  uint32_t out[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const uint32_t lo = v[2 * h], hi = v[2 * h + 1];
-    out[h] = code_byte(__uint_as_float(lo << 16) / scale) |
-             (code_byte(__uint_as_float(lo & 0xFFFF0000u) / scale) << 8) |
-             (code_byte(__uint_as_float(hi << 16) / scale) << 16) |
-             (code_byte(__uint_as_float(hi & 0xFFFF0000u) / scale) << 24);
-  }
-  reinterpret_cast<u32x2*>(a)[lane_id] = u32x2{out[0], out[1]};
+  reinterpret_cast<u32x2*>(a)[lane_id] = codes8(v, scale, 1.f / scale);
 }
 
 // One thread per block of 32, any alignment of x and a.

@@ -7,7 +7,8 @@
 // fl(x/scale) never exceeds 127 in magnitude for finite x, so the clamp only matters
 // for non-finite input; rounding uses the 1.5*2^23 add, whose low byte is the
 // two's-complement code and which maps NaN to 0 like the reference's
-// float->int conversion.
+// float->int conversion. The vector path takes the quotient from the row reciprocal and
+// divides only near half-integers (codes8 in ci8_device.h), with the same codes.
 //
 // Layout: one, two or four waves own a row (more for wider rows, so a lane holds at
 // most a few 16-byte packs) and keep it in registers between the max reduction and the
@@ -25,11 +26,6 @@ __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int offset = 32; offset >= 1; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, kWave));
   return v;
-}
-
-// rne(q) for |q| <= 127.5 as the low byte of fl(q + 1.5*2^23); NaN -> 0.
-__device__ __forceinline__ uint32_t code_byte(float q) {
-  return __float_as_uint(q + 12582912.0f) & 0xFFu;
 }
 
 // Vector path. Requires k % 8 == 0, x 16-byte aligned, codes 8-byte aligned.
@@ -75,29 +71,14 @@ __global__ void __launch_bounds__(256) quantize_rows_vec_kernel(
   }
   if (!active) return;
   const float scale = fmaxf(amax / 127.f, 1e-20f);
+  const float inv = 1.f / scale;
   if (part == 0 && lane == 0) scales[out_row] = scale;
   int8_t* dst = codes + int64_t(out_row) * k;
 #pragma unroll
   for (int i = 0; i < kPacks; ++i) {
     const int col = ((i * kWaves + part) * kWave + lane) * 8;
-    if (col < k) {
-      uint32_t out[2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        uint32_t bytes = 0;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const uint32_t word = packed[i][h * 2 + j];
-          const float lo = __uint_as_float(word << 16) / scale;
-          const float hi = __uint_as_float(word & 0xFFFF0000u) / scale;
-          bytes |= code_byte(lo) << (16 * j);
-          bytes |= code_byte(hi) << (16 * j + 8);
-        }
-        out[h] = bytes;
-      }
-      // Codes are not re-read by this kernel: stream them past the caches.
-      __builtin_nontemporal_store(u32x2{out[0], out[1]}, reinterpret_cast<u32x2*>(dst + col));
-    }
+    if (col < k)  // codes are not re-read by this kernel: stream them past the caches
+      __builtin_nontemporal_store(codes8(packed[i], scale, inv), reinterpret_cast<u32x2*>(dst + col));
   }
 }
 

@@ -80,66 +80,21 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-__device__ __forceinline__ uint32_t code_byte(float q) {
-  return __float_as_uint(q + 12582912.0f) & 0xFFu;  // rne(q) for |q| <= 127.5; NaN -> 0
-}
-
-__device__ __forceinline__ float lo_half(uint32_t word) { return __uint_as_float(word << 16); }
-__device__ __forceinline__ float hi_half(uint32_t word) {
-  return __uint_as_float(word & 0xFFFF0000u);
-}
-
 // Eight BF16 activations (four packed words) from eight gate and eight up values.
 __device__ __forceinline__ u32x4 swiglu8(const u32x4& gate, const u32x4& up) {
   u32x4 out;
   bool outside = false;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const float g0 = lo_half(gate[j]), g1 = hi_half(gate[j]);
+    const float g0 = bf16_lo(gate[j]), g1 = bf16_hi(gate[j]);
     outside |= !(fabsf(g0) < 87.f) | !(fabsf(g1) < 87.f);
-    out[j] = pack_bf16x2(swiglu_fast(g0, lo_half(up[j])), swiglu_fast(g1, hi_half(up[j])));
+    out[j] = pack_bf16x2(swiglu_fast(g0, bf16_lo(up[j])), swiglu_fast(g1, bf16_hi(up[j])));
   }
   if (outside) {  // |g| >= 87, infinite or NaN gates (essentially never in practice)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      out[j] = pack_bf16x2(swiglu_exact(lo_half(gate[j]), lo_half(up[j])),
-                           swiglu_exact(hi_half(gate[j]), hi_half(up[j])));
-  }
-  return out;
-}
-
-// Codes of eight BF16 values (four packed words) for a row scale, as two words of four
-// bytes: code = rne(fl(v / scale)) with the IEEE quotient, the low byte of the
-// 1.5 * 2^23 add. The quotient comes from q0 = fl(v * inv), inv = fl(1 / scale): for
-// |v / scale| < 128 (every finite v of the row), |q0 - v/scale| <= 2^-17 + 2^-17 and
-// |fl(v/scale) - v/scale| <= 2^-17, so when q0 is more than 2^-15 from every
-// half-integer, fl(v / scale) lies on the same side of each and rounds to the same
-// integer. Lanes with a value inside that band (about 1 in 16000 values) take the
-// division. NaN and infinite products give NaN, whose code is 0 as with the division.
-__device__ __forceinline__ u32x2 codes8(const u32x4& act, float scale, float inv) {
-  float q[8];
-  bool near = false;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    q[2 * j] = lo_half(act[j]) * inv;
-    q[2 * j + 1] = hi_half(act[j]) * inv;
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) near |= fabsf(q[j] - __builtin_floorf(q[j]) - 0.5f) <= 0x1p-15f;
-  if (near) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      q[2 * j] = lo_half(act[j]) / scale;
-      q[2 * j + 1] = hi_half(act[j]) / scale;
-    }
-  }
-  u32x2 out;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    uint32_t bytes = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bytes |= code_byte(q[4 * h + j]) << (8 * j);
-    out[h] = bytes;
+      out[j] = pack_bf16x2(swiglu_exact(bf16_lo(gate[j]), bf16_lo(up[j])),
+                           swiglu_exact(bf16_hi(gate[j]), bf16_hi(up[j])));
   }
   return out;
 }
@@ -169,7 +124,7 @@ __global__ void __launch_bounds__(64 * kWaves) silu_mul_quantize_kernel(
                        *reinterpret_cast<const u32x4*>(up + col));
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      amax = fmaxf(amax, fmaxf(fabsf(lo_half(act[i][j])), fabsf(hi_half(act[i][j]))));
+      amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(act[i][j])), fabsf(bf16_hi(act[i][j]))));
   }
   amax = wave_max(amax);
   if (lane == 0) partial[wave] = amax;

@@ -1,11 +1,13 @@
-"""CPU checks of the two arithmetic shortcuts in csrc/silu.hip, in numpy float32
-(IEEE round-to-nearest-even, the rounding of v_mul_f32 and of the IEEE division).
+"""CPU checks of two arithmetic shortcuts of the kernels, in numpy float32 (IEEE
+round-to-nearest-even, the rounding of v_mul_f32 and of the IEEE division).
 
-1. Codes from the row reciprocal: with inv = fl(1/scale), q0 = fl(v * inv) rounds to
-   the same integer as fl(v / scale) whenever q0 is more than 2^-15 from every
-   half-integer; the kernel divides for the other values.
-2. Reach of the fast path: for |g| < 87, 1 + e^-g stays below 2^126, so its reciprocal
-   is a normal number.
+1. Codes from the row reciprocal (codes8 in csrc/ci8_device.h, used by quantize_rows,
+   quantize_grouped4096, silu_mul_quantize and quantize_block32): with
+   inv = fl(1/scale), q0 = fl(v * inv) rounds to the same integer as fl(v / scale)
+   whenever q0 is more than 2^-15 from every half-integer; the kernels divide for the
+   other values.
+2. Reach of the SwiGLU fast path (csrc/silu.hip): for |g| < 87, 1 + e^-g stays below
+   2^126, so its reciprocal is a normal number.
 """
 
 import numpy as np
