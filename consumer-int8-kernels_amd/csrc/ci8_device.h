@@ -23,9 +23,11 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
 __device__ __forceinline__ uint32_t f32_to_bf16(float value) {
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(value));
 }
-// Two FP32 -> packed BF16 pair (low half = first).
+// Two FP32 -> packed BF16 pair (low half = first), one v_cvt_pk_bf16_f32 (RNE).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
 // Low and high BF16 halves of a packed pair, widened to FP32 (exact).

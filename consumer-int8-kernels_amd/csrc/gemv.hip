@@ -12,8 +12,9 @@
 // Design: the op is HBM-bound on the INT8 weights (N*K bytes).
 //  * The multiply-accumulate runs on v_mfma_f32_16x16x32_bf16 (rows = 16 channels,
 //    columns = up to 16 batch rows, so m <= 16 costs the same as m = 1). The VALU only
-//    dequantizes: XOR 0x80 (one op per four weights), v_cvt_f32_ubyteN, one FMA
-//    u*s - 128*s (exact, since code*scale fits in FP32), and v_cvt_pk_bf16_f32.
+//    dequantizes, 2.5 instructions per weight: a sign-extending v_cvt_f32_i32 with SDWA
+//    byte select, one multiply by the scale (exact, since code*scale fits in FP32) and
+//    half a v_cvt_pk_bf16_f32.
 //  * A workgroup owns kCB blocks of 16 channels and splits K into kS contiguous
 //    ranges; each of its kCB*kS waves streams one (block, range) pair of W straight
 //    from HBM into registers, two stages of kU 64-byte K blocks ahead of its MFMAs.
@@ -51,12 +52,12 @@ struct GemvConfig {
   static_assert(8 % kU == 0, "a copy instruction covers whole x rows");
 };
 
-__device__ __forceinline__ uint32_t dequant_pair(uint32_t word, int shift, float s,
-                                                 float bias) {
-  // word holds (code + 128) bytes; bytes `shift/8` and `shift/8 + 1` are converted.
-  const float lo = fmaf(float((word >> shift) & 0xFFu), s, bias);
-  const float hi = fmaf(float((word >> (shift + 8)) & 0xFFu), s, bias);
-  return pack_bf16x2(lo, hi);
+// Four INT8 codes -> two packed BF16 pairs bf16_rn(code * s). code * s is exact in FP32
+// (8-bit by 8-bit significands), so the one rounding is the BF16 one. Each byte is
+// sign-extended and converted by one v_cvt_f32_i32 (SDWA byte select).
+__device__ __forceinline__ u32x2 dequant4(uint32_t word, float s) {
+  return u32x2{pack_bf16x2(float(int8_t(word)) * s, float(int8_t(word >> 8)) * s),
+               pack_bf16x2(float(int8_t(word >> 16)) * s, float(int8_t(word >> 24)) * s)};
 }
 
 __device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
@@ -132,7 +133,7 @@ __device__ __forceinline__ void gemv_stage(int t, const XCopies<C>& xc,
                                            lds_char* const (&xs)[3], u32x4 (&wv)[3][C::kU],
                                            f32x4& acc, int wave, uint32_t w_base, int group,
                                            int row, int range, int range_len, int kblocks,
-                                           int k, float s, float bias) {
+                                           int k, float s) {
   waitcnt<vmcnt_imm(C::kU)>();  // everything but W(t+1) has landed, x(t) included
   workgroup_barrier();          // every wave's share of x(t) has landed
   const lds_char* base = xs[R] + (range * 16 + row) * C::kRowBytes;
@@ -151,11 +152,8 @@ __device__ __forceinline__ void gemv_stage(int t, const XCopies<C>& xc,
     const u32x4 wq = wv[R][j];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const uint32_t w0 = wq[2 * h] ^ 0x80808080u;
-      const uint32_t w1 = wq[2 * h + 1] ^ 0x80808080u;
-      acc = mfma_bf16(u32x4{dequant_pair(w0, 0, s, bias), dequant_pair(w0, 16, s, bias),
-                            dequant_pair(w1, 0, s, bias), dequant_pair(w1, 16, s, bias)},
-                      xf[j][h], acc);
+      const u32x2 lo = dequant4(wq[2 * h], s), hi = dequant4(wq[2 * h + 1], s);
+      acc = mfma_bf16(u32x4{lo[0], lo[1], hi[0], hi[1]}, xf[j][h], acc);
     }
   }
 }
@@ -180,7 +178,6 @@ __global__ void __launch_bounds__(C::kThreads) channel_gemv_kernel(
   const auto w_rsrc = make_rsrc(w, uint32_t(n) * uint32_t(k));
   const auto x_rsrc = make_rsrc(x, uint32_t(m) * uint32_t(k) * 2u);
   const float s = channel < n ? bf16_to_f32(scale[channel]) : 0.f;
-  const float bias = -128.f * s;
   const uint32_t w_base =
       channel < n ? uint32_t(channel) * uint32_t(k) + uint32_t(group * 16) : kOutOfRange;
   const int kblocks = (k + 63) / 64;
@@ -207,13 +204,13 @@ __global__ void __launch_bounds__(C::kThreads) channel_gemv_kernel(
   issue_w<C>(wv[1], w_rsrc, w_base, group * 16, range, 1, range_len, kblocks, k);
   for (int t = 0; t < stages; t += 3) {
     gemv_stage<C, 0>(t, xc, x_rsrc, w_rsrc, xs, wv, acc, wave, w_base, group, row, range,
-                     range_len, kblocks, k, s, bias);
+                     range_len, kblocks, k, s);
     if (t + 1 >= stages) break;
     gemv_stage<C, 1>(t + 1, xc, x_rsrc, w_rsrc, xs, wv, acc, wave, w_base, group, row, range,
-                     range_len, kblocks, k, s, bias);
+                     range_len, kblocks, k, s);
     if (t + 2 >= stages) break;
     gemv_stage<C, 2>(t + 2, xc, x_rsrc, w_rsrc, xs, wv, acc, wave, w_base, group, row, range,
-                     range_len, kblocks, k, s, bias);
+                     range_len, kblocks, k, s);
   }
   waitcnt<vmcnt_imm(0)>();  // drain the trailing (out-of-range) copies before exit
 
@@ -234,104 +231,67 @@ __global__ void __launch_bounds__(C::kThreads) channel_gemv_kernel(
 
 
 // ---------------------------------------------------------------------------------
-// Small-batch variant: x resident in LDS. The LDS holds x[0:m, :] as rows of kblocks
-// 128-byte blocks (16-byte chunks XOR-swizzled by row & 7) followed by 1 KiB of zeros;
-// lanes for batch rows >= m, and K blocks past a wave's range, read the zeros. Wave
-// (cb, range) streams 16 channels x its K range of W, kAhead stages of kU blocks ahead.
-template <int kCB_, int kS_, int kU_, int kAhead_>
+// Small-batch variant: x resident in LDS, W streamed with a rolling per-wave window.
+//
+// A workgroup owns one block of 16 channels and kS waves; wave r sums K range r. The
+// LDS holds x[0:m, :] as rows of kblocks 128-byte blocks (16-byte chunks XOR-swizzled
+// by row & 7), copied once by buffer_load ... lds. Each wave keeps kAhead 64-byte K
+// blocks of its W rows in flight and refills a slot right after its MFMAs, so the
+// memory pipe never drains between stages:
+//  * every wait is explicit and partial: the x copies are issued before the W
+//    prologue and waited for with vmcnt(kAhead), then a bare s_barrier (no fence, so
+//    the W loads stay in flight); inside the loop each slot waits for vmcnt(kAhead-1);
+//  * the loop has no early exit and a scheduling barrier after each slot, so the
+//    compiler neither sinks refills behind a branch nor hoists later slots' MFMAs
+//    above earlier slots' refills;
+//  * slots past the wave's K range load nothing (range-checked offset) and skip their
+//    MFMAs on a wave-uniform branch;
+//  * the channel scale is read by a range-checked buffer load (zero past N), so no
+//    branch forces a wait before the first W load is issued.
+// Batch rows past m read x row m-1 and channels past N re-read row N-1: both feed only
+// MFMA output rows/columns that are never stored, so no zero padding is needed. x
+// chunks past K are copied as zeros, which also cancels the next row's bytes that a
+// K tail (K % 64 != 0) reads into the last block.
+template <int kS_, int kAhead_, int kWavesPerEU_>
 struct ResidentConfig {
-  static constexpr int kCB = kCB_, kS = kS_, kU = kU_, kAhead = kAhead_;
-  static constexpr int kWaves = kCB * kS;
-  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kS = kS_, kAhead = kAhead_;
+  static constexpr int kWavesPerEU = kWavesPerEU_;  // 8: at most 64 VGPRs, 32 waves per CU
+  static constexpr int kThreads = 64 * kS;
 };
 
-inline int resident_lds_bytes(int m, int k) { return m * ((k + 63) / 64) * 128 + 1024; }
-
-template <class C, int R>
-__device__ __forceinline__ void resident_stage(int t, __amdgpu_buffer_rsrc_t w_rsrc,
-                                               uint32_t w_base, int lane_col, int kb_first,
-                                               int kend, int k, u32x4 (&wv)[C::kAhead][C::kU],
-                                               f32x4& acc, const lds_char* xs,
-                                               bool row_live, uint32_t x_row, uint32_t x_zero,
-                                               int group, int row, float s, float bias) {
-  waitcnt<vmcnt_imm((C::kAhead - 1) * C::kU)>();  // W(t) landed, later stages in flight
-#pragma unroll
-  for (int j = 0; j < C::kU; ++j) {
-    const int kb = kb_first + t * C::kU + j;  // wave-uniform
-    // Batch rows >= m and blocks past this wave's range read the zero KiB.
-    const uint32_t base = row_live && kb < kend ? x_row + uint32_t(kb * 128) : x_zero;
-    u32x4 xf[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      xf[h] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
-          xs + base + (((2 * group + h) ^ (row & 7)) * 16));
-    const u32x4 wq = wv[R][j];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t w0 = wq[2 * h] ^ 0x80808080u;
-      const uint32_t w1 = wq[2 * h + 1] ^ 0x80808080u;
-      acc = mfma_bf16(u32x4{dequant_pair(w0, 0, s, bias), dequant_pair(w0, 16, s, bias),
-                            dequant_pair(w1, 0, s, bias), dequant_pair(w1, 16, s, bias)},
-                      xf[h], acc);
-    }
-  }
-  // Refill this register slot with stage t + kAhead.
-#pragma unroll
-  for (int j = 0; j < C::kU; ++j) {
-    const int kb = kb_first + (t + C::kAhead) * C::kU + j;
-    const bool valid = kb < kend && kb * 64 + lane_col < k;
-    wv[R][j] = __builtin_bit_cast(
-        u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                   w_rsrc, valid ? w_base + uint32_t(kb * 64) : kOutOfRange, 0, 0));
-  }
+__host__ __device__ inline int resident_lds_bytes(int m, int k) {
+  return m * ((k + 63) / 64) * 128 + 1024;  // + one spill KiB for the last copy
 }
 
 template <class C>
-__global__ void __launch_bounds__(C::kThreads) channel_gemv_resident_kernel(
+__global__ void __launch_bounds__(C::kThreads, C::kWavesPerEU) channel_gemv_resident_kernel(
     const uint16_t* __restrict__ x, const int8_t* __restrict__ w,
     const uint16_t* __restrict__ scale, uint16_t* __restrict__ out, int m, int n, int k) {
-  static_assert(C::kAhead == 3, "the stage loop below is unrolled for three slots");
   extern __shared__ __attribute__((aligned(1024))) char xs_raw[];
-  __shared__ f32x4 partial[C::kWaves][64];
+  __shared__ f32x4 partial[C::kS][64];
   const lds_char* xs = (const lds_char*)xs_raw;
 
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int cb = wave % C::kCB, range = wave / C::kCB;
+  const int range = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row = lane & 15, group = lane >> 4;
-  const int channel = blockIdx.x * 16 * C::kCB + cb * 16 + row;
+  const int channel = blockIdx.x * 16 + row;
 
   const auto w_rsrc = make_rsrc(w, uint32_t(n) * uint32_t(k));
   const auto x_rsrc = make_rsrc(x, uint32_t(m) * uint32_t(k) * 2u);
-  const float s = channel < n ? bf16_to_f32(scale[channel]) : 0.f;
-  const float bias = -128.f * s;
-  const uint32_t w_base =
-      channel < n ? uint32_t(channel) * uint32_t(k) + uint32_t(group * 16) : kOutOfRange;
+  const auto s_rsrc = make_rsrc(scale, uint32_t(n) * 2u);
+  const uint32_t s_bits = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, uint32_t(channel) * 2u, 0, 0);
+  const uint32_t w_lane = uint32_t(min(channel, n - 1)) * uint32_t(k) + uint32_t(group * 16);
   const int kblocks = (k + 63) / 64;
   const int range_len = (kblocks + C::kS - 1) / C::kS;
   const int kb_first = range * range_len;
   const int kend = min(kb_first + range_len, kblocks);
-  const int stages = (range_len + C::kU - 1) / C::kU;
+  const int groups = (range_len + C::kAhead - 1) / C::kAhead;
 
-  // W first (the long-latency stream): stages 0 .. kAhead-1.
-  u32x4 wv[C::kAhead][C::kU];
-#pragma unroll
-  for (int a = 0; a < C::kAhead; ++a)
-#pragma unroll
-    for (int j = 0; j < C::kU; ++j) {
-      const int kb = kb_first + a * C::kU + j;
-      const bool valid = kb < kend && kb * 64 + group * 16 < k;
-      wv[a][j] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                     w_rsrc, valid ? w_base + uint32_t(kb * 64) : kOutOfRange, 0, 0));
-    }
-
-  // Copy x: 16-byte unit u of LDS row r holds global chunk (u % 8) ^ (r & 7) of block
-  // u / 8. The last copy may spill past the rows into the zero KiB, writing zeros.
+  // x copy: 16-byte unit u of LDS row r holds global chunk (u % 8) ^ (r & 7) of block
+  // u / 8. The last copy may spill up to 1 KiB past the rows, writing zeros.
   const int row_units = kblocks * 8;
   const int units = m * row_units;
-  const uint32_t zero_off = uint32_t(units) * 16u;
-  for (int u0 = wave * 64; u0 < units; u0 += C::kWaves * 64) {
+  for (int u0 = range * 64; u0 < units; u0 += C::kThreads) {
     const int u = u0 + lane;
     const int r = u / row_units, within = u % row_units;
     const int kb = within >> 3, c = (within & 7) ^ (r & 7);
@@ -339,36 +299,58 @@ __global__ void __launch_bounds__(C::kThreads) channel_gemv_resident_kernel(
     copy16(x_rsrc, reinterpret_cast<lds_void*>((lds_char*)xs_raw + u0 * 16),
            valid ? uint32_t(r) * uint32_t(k) * 2u + uint32_t(kb * 128 + c * 16) : kOutOfRange);
   }
-  for (int i = threadIdx.x; i < 64; i += C::kThreads)
-    reinterpret_cast<u32x4*>(xs_raw + zero_off)[i] = u32x4{0, 0, 0, 0};
-  waitcnt<vmcnt_imm(0)>();
-  __syncthreads();
 
-  const bool row_live = row < m;
-  const uint32_t x_row = uint32_t(row * kblocks * 128);
+  // W prologue: slots 0 .. kAhead-1, in slot order.
+  u32x4 wv[C::kAhead];
+#pragma unroll
+  for (int a = 0; a < C::kAhead; ++a) {
+    const int kb = kb_first + a;
+    wv[a] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                          w_rsrc, kb < kend ? w_lane + uint32_t(kb * 64) : kOutOfRange, 0, 0));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  waitcnt<vmcnt_imm(C::kAhead)>();  // the scale and this wave's x copies have landed
+  workgroup_barrier();              // every wave's x copies have landed
+
+  const float s = bf16_to_f32(s_bits);
+  const int xr = min(row, m - 1);
+  const lds_char* x_lane = xs + xr * kblocks * 128 + kb_first * 128;
+  const int swz0 = ((2 * group) ^ (xr & 7)) * 16, swz1 = ((2 * group + 1) ^ (xr & 7)) * 16;
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int t = 0; t < stages; t += 3) {
-    resident_stage<C, 0>(t, w_rsrc, w_base, group * 16, kb_first, kend, k, wv, acc, xs,
-                         row_live, x_row, zero_off, group, row, s, bias);
-    if (t + 1 >= stages) break;
-    resident_stage<C, 1>(t + 1, w_rsrc, w_base, group * 16, kb_first, kend, k, wv, acc, xs,
-                         row_live, x_row, zero_off, group, row, s, bias);
-    if (t + 2 >= stages) break;
-    resident_stage<C, 2>(t + 2, w_rsrc, w_base, group * 16, kb_first, kend, k, wv, acc, xs,
-                         row_live, x_row, zero_off, group, row, s, bias);
+  for (int g = 0; g < groups; ++g) {
+#pragma unroll
+    for (int a = 0; a < C::kAhead; ++a) {
+      const int slot = g * C::kAhead + a;   // wave-uniform
+      const int kb = kb_first + slot;
+      waitcnt<vmcnt_imm(C::kAhead - 1)>();  // slot a's W has landed
+      if (kb < kend) {
+        const lds_char* xb = x_lane + slot * 128;
+        const u32x4 x0 = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xb + swz0);
+        const u32x4 x1 = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xb + swz1);
+        const u32x4 wq = wv[a];
+        const u32x2 d0 = dequant4(wq[0], s), d1 = dequant4(wq[1], s);
+        const u32x2 d2 = dequant4(wq[2], s), d3 = dequant4(wq[3], s);
+        acc = mfma_bf16(u32x4{d0[0], d0[1], d1[0], d1[1]}, x0, acc);
+        acc = mfma_bf16(u32x4{d2[0], d2[1], d3[0], d3[1]}, x1, acc);
+      }
+      const int next = kb + C::kAhead;
+      wv[a] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            w_rsrc, next < kend ? w_lane + uint32_t(next * 64) : kOutOfRange, 0, 0));
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   waitcnt<vmcnt_imm(0)>();  // drain the trailing (out-of-range) loads before exit
 
-  partial[wave][lane] = acc;
+  partial[range][lane] = acc;
   __syncthreads();
-  for (int slot = threadIdx.x; slot < C::kCB * 64 * 4; slot += C::kThreads) {
-    const int e = slot & 3, l = (slot >> 2) & 63, b = slot >> 8;
+  for (int slot = threadIdx.x; slot < 64 * 4; slot += C::kThreads) {
+    const int e = slot & 3, l = slot >> 2;
     const int out_row = l & 15;
-    const int out_col = blockIdx.x * 16 * C::kCB + b * 16 + (l >> 4) * 4 + e;
+    const int out_col = blockIdx.x * 16 + (l >> 4) * 4 + e;
     if (out_row >= m || out_col >= n) continue;
-    float sum = partial[b][l][e];
+    float sum = partial[0][l][e];
 #pragma unroll
-    for (int v = 1; v < C::kS; ++v) sum += partial[v * C::kCB + b][l][e];
+    for (int v = 1; v < C::kS; ++v) sum += partial[v][l][e];
     out[int64_t(out_row) * n + out_col] = uint16_t(f32_to_bf16(sum));
   }
 }
@@ -381,9 +363,9 @@ hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale
   // ranges wins for m <= 4; above that the LDS copy limits occupancy and the ring with
   // 2 channel blocks x 2 K ranges and 4-block stages is faster.
   const int lds = resident_lds_bytes(m, k);
-  if (m <= 4 && lds <= 60 * 1024) {  // plus 4 KiB of static LDS: within the 64 KiB default
-    using R = ResidentConfig<1, 4, 4, 3>;
-    const int grid = (n + 16 * R::kCB - 1) / (16 * R::kCB);
+  if (m <= 4 && lds <= 56 * 1024) {  // plus 8 KiB of static LDS: within the 64 KiB default
+    using R = ResidentConfig<8, 10, 8>;
+    const int grid = (n + 15) / 16;
     channel_gemv_resident_kernel<R><<<grid, R::kThreads, lds, stream>>>(
         static_cast<const uint16_t*>(x), w, static_cast<const uint16_t*>(scale),
         static_cast<uint16_t*>(out), m, n, k);
