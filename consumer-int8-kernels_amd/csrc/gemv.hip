@@ -28,8 +28,9 @@
 //    arrays so the compiler can see that the slot being read is not the slot an
 //    in-flight copy is writing.
 // For small batches (m <= 4, x small enough to sit in LDS) a second kernel copies all
-// of x into LDS once and then lets every wave stream its W with three stages of loads
-// in flight and no barriers at all, which removes the per-stage lock-step of the ring.
+// of x into LDS once and then lets every wave stream its W through a rolling window of
+// ten 64-byte blocks with no barriers at all, which removes the per-stage lock-step of
+// the ring.
 // Weight rows past N and K chunks past K read as zero through the buffer range check.
 #include "ci8_device.h"
 #include "launch.h"
@@ -359,9 +360,10 @@ __global__ void __launch_bounds__(C::kThreads, C::kWavesPerEU) channel_gemv_resi
 
 hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale, void* out,
                                int m, int n, int k, hipStream_t stream) {
-  // Measured on MI355X at K=5120, N=17408: x resident in LDS with 1 channel block x 4 K
-  // ranges wins for m <= 4; above that the LDS copy limits occupancy and the ring with
-  // 2 channel blocks x 2 K ranges and 4-block stages is faster.
+  // Measured on MI355X at K=5120, N=17408: x resident in LDS with 8 K ranges per block of
+  // 16 channels and a 10-block window wins for m <= 4; above that the LDS copy limits
+  // occupancy and the ring with 2 channel blocks x 2 K ranges and 4-block stages is
+  // faster.
   const int lds = resident_lds_bytes(m, k);
   if (m <= 4 && lds <= 56 * 1024) {  // plus 8 KiB of static LDS: within the 64 KiB default
     using R = ResidentConfig<8, 10, 8>;
