@@ -9,7 +9,9 @@ GEMM. Inputs are resident in HBM before timing; the weights, activations and cod
 rotate over enough copies that no step finds its inputs in the 256 MB Infinity Cache.
 
 Also reported: `roofline` for the dominant kernel (the GEMM, timed per launch with HIP
-events on the stream it runs on); extra roofline lines for the quantizer, the W8A16
+events on the stream it runs on); `mfma_probe`, the INT8 MFMA rate and shader clock
+under a full-chip pure-MFMA loop, with the dense INT8 peak at that measured clock
+(`roofline.frac_at_measured_clock` divides by it); extra roofline lines for the quantizer, the W8A16
 GEMV, the grouped summed GEMM, the biased-UINT8 down
 projection with its SwiGLU activation producers (silu_mul_quantize,
 silu_mul) and the AllSpark weight restore (unpack_allspark), and the small quantize +
@@ -101,6 +103,36 @@ def time_kernel(torch, calls, reps, batch=10):
     torch.cuda.synchronize()
     times = [s.elapsed_time(e) * 1e3 / batch for s, e in events]
     return statistics.mean(times), statistics.median(times)
+
+
+def mfma_clock_probe(torch, cus: int, rounds: int = 4000, reps: int = 5) -> dict:
+    """INT8 MFMA rate and shader clock under a full-chip pure-MFMA load (one workgroup of
+    4 waves per CU, csrc/probe.hip), and the dense INT8 peak at that measured clock."""
+    import ctypes
+
+    lib = ctypes.CDLL(str(REPO / "consumer-int8-kernels_amd" / "consumer_int8" / "libci8_probe.so"))
+    lib.ci8probe_mfma_loop.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.ci8probe_ops_per_mfma.restype = ctypes.c_int64
+    shader_khz, wall_khz = ctypes.c_int(0), ctypes.c_int(0)
+    assert lib.ci8probe_clock_rates(ctypes.byref(shader_khz), ctypes.byref(wall_khz)) == 0
+    record = torch.zeros(3 * cus, dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    ops = cus * 4 * rounds * lib.ci8probe_mfma_per_round() * lib.ci8probe_ops_per_mfma()
+    assert lib.ci8probe_mfma_loop(rounds // 10, cus, ctypes.c_void_p(record.data_ptr()), ctypes.c_void_p(stream)) == 0
+    tops, mhz = [], []
+    for _ in range(reps):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        assert lib.ci8probe_mfma_loop(rounds, cus, ctypes.c_void_p(record.data_ptr()), ctypes.c_void_p(stream)) == 0
+        end.record()
+        torch.cuda.synchronize()
+        tops.append(ops / (start.elapsed_time(end) * 1e-3) / 1e12)
+        rec = record.view(cus, 3).cpu()
+        mhz.append(statistics.median((rec[:, 0].double() / rec[:, 1].double() * wall_khz.value / 1e3).tolist()))
+    clock = statistics.median(mhz)
+    return {"tops": round(statistics.median(tops), 1), "clock_mhz": round(clock, 1),
+            "clock_mhz_max": shader_khz.value / 1e3,
+            "peak_at_clock_tops": round(cus * 8192 * clock * 1e6 / 1e12, 1)}
 
 
 def cpu_baseline(budget_s: float) -> dict:
@@ -226,6 +258,11 @@ def main() -> int:
         },
         "device": {"name": props.name, "cus": cus, "gcn_arch": getattr(props, "gcnArchName", "")},
     }
+    # The nominal peak above assumes 2.4 GHz. The probe measures the clock the chip holds
+    # under a full-chip MFMA load and the dense INT8 peak at that clock.
+    probe = mfma_clock_probe(torch, cus)
+    result["mfma_probe"] = probe
+    result["roofline"]["frac_at_measured_clock"] = round(gemm_tops / probe["peak_at_clock_tops"], 4)
 
     if not args.no_extras:
         extras = {}

@@ -1,8 +1,9 @@
 """Build the gfx950 library and the torch op module in-tree.
 
 Outputs (next to the Python package, so they travel with the source tree):
-  consumer_int8/libci8_amd.so  -- HIP kernels + the C ABI of include/consumer_int8_amd.h
-  consumer_int8/_C.so          -- torch.ops.consumer_int8.* registration (stable ABI)
+  consumer_int8/libci8_amd.so   -- HIP kernels + the C ABI of include/consumer_int8_amd.h
+  consumer_int8/_C.so           -- torch.ops.consumer_int8.* registration (stable ABI)
+  consumer_int8/libci8_probe.so -- bench.py's MFMA-loop clock probe (not the drop-in)
 
 Usage: python consumer-int8-kernels_amd/build.py   (or __graft_entry__.build()).
 hipcc cross-compiles for gfx950, so this runs on a machine without a GPU.
@@ -57,7 +58,8 @@ def _run(cmd: list[str]) -> None:
 # register allocator rotate the 224 MFMA accumulators between AGPRs and VGPRs in the
 # software-pipelined loop (copies around every MFMA); iterative-minreg keeps every
 # accumulator in place.
-FILE_FLAGS = {"gemm.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-minreg"]}
+FILE_FLAGS = {"gemm.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-minreg"],
+              "probe.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-minreg"]}
 
 
 def _compile(src: Path, obj: Path) -> Path:
@@ -84,6 +86,19 @@ def build_library(jobs: int = 8) -> Path:
     return target
 
 
+def build_probe() -> Path:
+    obj = BUILD_DIR / "probe.o"
+    BUILD_DIR.mkdir(exist_ok=True)
+    _compile(CSRC / "probe.hip", obj)
+    target = OUT_DIR / "libci8_probe.so"
+    tmp = target.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), str(obj),
+          f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}",
+          "-Wl,-soname,libci8_probe.so"])
+    os.replace(tmp, target)
+    return target
+
+
 def build_torch_module() -> Path:
     import torch  # noqa: PLC0415  (only the build needs torch's headers)
 
@@ -104,6 +119,7 @@ def build_torch_module() -> Path:
 
 def build() -> None:
     build_library()
+    build_probe()
     build_torch_module()
 
 
