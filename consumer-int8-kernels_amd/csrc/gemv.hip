@@ -27,10 +27,10 @@
 //  * One barrier per stage. The ring has three slots, held in three separate LDS
 //    arrays so the compiler can see that the slot being read is not the slot an
 //    in-flight copy is writing.
-// For small batches (m <= 4, x small enough to sit in LDS) a second kernel copies all
-// of x into LDS once and then lets every wave stream its W through a rolling window of
-// ten 64-byte blocks with no barriers at all, which removes the per-stage lock-step of
-// the ring.
+// For small batches (x[0:m, :] within 72 KiB of LDS: m <= 6 at K = 5120) a second kernel
+// copies all of x into LDS once and then lets every wave stream its W through a rolling
+// window of ten 64-byte blocks with no barriers at all, which removes the per-stage
+// lock-step of the ring.
 // Weight rows past N and K chunks past K read as zero through the buffer range check.
 #include "ci8_device.h"
 #include "launch.h"
@@ -361,14 +361,24 @@ __global__ void __launch_bounds__(C::kThreads, C::kWavesPerEU) channel_gemv_resi
 hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale, void* out,
                                int m, int n, int k, hipStream_t stream) {
   // Measured on MI355X at K=5120, N=17408: x resident in LDS with 8 K ranges per block of
-  // 16 channels and a 10-block window wins for m <= 4; above that the LDS copy limits
-  // occupancy and the ring with 2 channel blocks x 2 K ranges and 4-block stages is
-  // faster.
+  // 16 channels and a 10-block window wins while two workgroups fit on a CU (m <= 6:
+  // 23.9 / 24.2 us at m = 5 / 6 against 25.2 / 25.4 us for the ring); with one per CU
+  // (m = 8: 30.5 against 26.2 us) the ring with 2 channel blocks x 2 K ranges and
+  // 4-block stages is faster.
   const int lds = resident_lds_bytes(m, k);
-  if (m <= 4 && lds <= 56 * 1024) {  // plus 8 KiB of static LDS: within the 64 KiB default
+  if (lds <= 72 * 1024) {  // plus 8 KiB of static LDS: two workgroups per CU
     using R = ResidentConfig<8, 10, 8>;
+    auto kernel = channel_gemv_resident_kernel<R>;
+    static bool configured = false;  // benign race: every thread sets the same attribute
+    if (!configured && lds > 56 * 1024) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               72 * 1024);
+      if (e != hipSuccess) return e;
+      configured = true;
+    }
     const int grid = (n + 15) / 16;
-    channel_gemv_resident_kernel<R><<<grid, R::kThreads, lds, stream>>>(
+    kernel<<<grid, R::kThreads, lds, stream>>>(
         static_cast<const uint16_t*>(x), w, static_cast<const uint16_t*>(scale),
         static_cast<uint16_t*>(out), m, n, k);
     return hipGetLastError();

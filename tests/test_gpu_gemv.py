@@ -28,7 +28,7 @@ def check_gemv(out_bits, x_bits, w, s_bits):
     assert np.all(np.abs(actual - exact) <= bound)
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 8, 16])
 @pytest.mark.parametrize("n,k", [(37, 528), (512, 5120)])
 def test_w8a16_small_batch_matches_bf16_dequantized_linear(ops, m, n, k):
     rng = np.random.default_rng(134)
@@ -48,7 +48,7 @@ def test_w8a16_small_batch_matches_bf16_dequantized_linear(ops, m, n, k):
     check_gemv(bf16_bits(out), bf16_bits(x), w, s_bits)
 
 
-@pytest.mark.parametrize("m", [1, 4, 8, 16])
+@pytest.mark.parametrize("m", [1, 4, 6, 8, 16])
 def test_decode_shape_full_size(ops, m):
     """Config 2: K = 5120, N = 17408, scales uniform in [1e-3, 1e-2]."""
     k, n = 5120, 17408
