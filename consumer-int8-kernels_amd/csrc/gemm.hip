@@ -775,11 +775,71 @@ struct WLdsConfig {
   static constexpr int kStageBytes = BN * BK;
   static constexpr int kBlocks = kStageBytes / 1024;
   static constexpr int kLoads = kBlocks / kWaves;  // W DMA per wave per stage
-  static constexpr int kLdsBytes = kSlots * kStageBytes;
+  static constexpr int kRingBytes = kSlots * kStageBytes;
+  // Epilogue staging, reusing the ring: each wave's 64 x BN BF16 outputs at a row stride
+  // of BN*2 + 16 bytes (116 dwords for BN = 224: 116 = 4 x odd mod 64, so the 16 rows a
+  // ds_write_b64 covers start in distinct banks).
+  static constexpr int kEpiRowBytes = BN * 2 + 16;
+  static constexpr int kEpiWaveBytes = (BM / kWaves) * kEpiRowBytes;
+  static constexpr int kLdsBytes =
+      kRingBytes > kWaves * kEpiWaveBytes ? kRingBytes : kWaves * kEpiWaveBytes;
   static_assert(kLoads * kWaves == kBlocks, "whole 1 KiB W blocks per wave");
+  static_assert((BN * 2) % 16 == 0, "whole 16-byte output chunks per row");
   static_assert(TM * 16 * kWaves == BM && TN * 16 == BN, "wave tiling");
   static_assert(kLdsBytes <= 160 * 1024, "LDS");
 };
+
+// Epilogue of one wave's in-bounds 64 x BN tile through LDS. The scale arithmetic and
+// rounding are those of store_tile16; the BF16 results go to the wave's LDS region in
+// the MFMA layout (8 bytes per lane and block) and come back as 16-byte row chunks, so
+// each global store instruction writes whole 128-byte lines (consecutive lanes along a
+// row) instead of 16 rows x 32 bytes. Requires n % 8 == 0 and a 16-byte aligned out.
+template <class C>
+__device__ __forceinline__ void store_tile16_lds(const i32x4 (&acc)[C::TM][C::TN],
+                                                 char __attribute__((address_space(3)))* region,
+                                                 int row0, int col0, int n,
+                                                 const float* __restrict__ sa,
+                                                 const uint16_t* __restrict__ sw,
+                                                 uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int frag_row = lane & 15, frag_group = lane >> 4;
+  float row_scale[C::TM];
+#pragma unroll
+  for (int j = 0; j < C::TM; ++j) row_scale[j] = sa[row0 + j * 16 + frag_row];
+  u32x2 s2[C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TN; ++i)
+    s2[i] = *reinterpret_cast<const u32x2*>(sw + col0 + i * 16 + frag_group * 4);
+#pragma unroll
+  for (int j = 0; j < C::TM; ++j) {
+    auto* row_base = region + (j * 16 + frag_row) * C::kEpiRowBytes + frag_group * 8;
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i) {
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t sbits = (s2[i][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+        v[e] = (float(acc[j][i][e]) * row_scale[j]) * bf16_to_f32(sbits);
+      }
+      *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(row_base + i * 32) =
+          u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    }
+  }
+  // One wave's LDS operations complete in order; the wait only orders the reads after
+  // every lane's writes for the compiler.
+  __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+  __builtin_amdgcn_wave_barrier();
+  constexpr int kChunks = C::BN / 8;  // 16-byte chunks per output row
+  constexpr int kRows = C::BM / C::kWaves;
+#pragma unroll
+  for (int it = 0; it < kRows * kChunks / 64; ++it) {
+    const int q = it * 64 + lane;
+    const int row = q / kChunks, chunk = q % kChunks;
+    const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+        region + row * C::kEpiRowBytes + chunk * 16);
+    *reinterpret_cast<u32x4*>(out + int64_t(row0 + row) * n + col0 + chunk * 8) = v;
+  }
+}
 
 template <class C, WeightCode kCode, bool kWorkspace, bool kExactK>
 __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
@@ -971,8 +1031,19 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
   if (t + 1 < ns) stage(t + 1, 1);
   waitcnt<vmcnt_imm(0)>();  // copies past the last stage
 
-  store_tile16<C::TM, C::TN, kWorkspace>(acc, m0 + wave * (C::BM / C::kWaves), n0, m, n, sa, sw,
-                                        out, ws, vec_n);
+  const int row0 = m0 + wave * (C::BM / C::kWaves);
+  if constexpr (!kWorkspace) {
+    // Every wave's last ring reads and copies are done before any wave reuses the ring.
+    __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+    workgroup_barrier();
+    const bool lds_path = vec_n && n % 8 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
+                          row0 + C::TM * 16 <= m && n0 + C::TN * 16 <= n;
+    if (lds_path) {
+      store_tile16_lds<C>(acc, lds + wave * C::kEpiWaveBytes, row0, n0, n, sa, sw, out);
+      return;
+    }
+  }
+  store_tile16<C::TM, C::TN, kWorkspace>(acc, row0, n0, m, n, sa, sw, out, ws, vec_n);
 }
 
 template <class C, WeightCode kCode, bool kWorkspace, bool kExactK>
