@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace ci8 {
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
@@ -87,6 +89,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 }
 // An offset past every valid buffer (buffers are limited to INT_MAX bytes).
 constexpr uint32_t kOutOfRange = 0x80000000u;
+
+// Raises `kernel`'s dynamic LDS limit to `bytes` on the first call that succeeds. The
+// attribute is idempotent, so concurrent first calls may both set it; the flag is atomic.
+template <class Kernel>
+inline hipError_t raise_lds_limit_once(Kernel kernel, int bytes, std::atomic<bool>& done) {
+  if (done.load(std::memory_order_acquire)) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done.store(true, std::memory_order_release);
+  return e;
+}
 
 // s_waitcnt immediate that waits until at most `n` vector-memory operations are
 // outstanding and leaves the other counters unconstrained (gfx9 encoding).

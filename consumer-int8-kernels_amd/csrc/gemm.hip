@@ -330,14 +330,9 @@ template <class C, WeightCode kCode, bool kWorkspace>
 hipError_t run(const int8_t* a, const void* w, const float* sa, const void* sw, void* out,
                int32_t* ws, int m, int n, int k, hipStream_t stream) {
   auto kernel = channel_gemm_kernel<C, kCode, kWorkspace>;
-  static bool configured = false;  // benign race: every thread sets the same attribute
-  if (!configured) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             C::kLdsBytes);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
+  static std::atomic<bool> configured{false};
+  if (const hipError_t e = raise_lds_limit_once(kernel, C::kLdsBytes, configured); e != hipSuccess)
+    return e;
   const int blocks = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
   const bool vec_n = n % 4 == 0 && reinterpret_cast<uintptr_t>(sw) % 8 == 0 &&
                      reinterpret_cast<uintptr_t>(out) % 8 == 0 &&
@@ -1050,14 +1045,9 @@ template <class C, WeightCode kCode, bool kWorkspace, bool kExactK>
 hipError_t run_wlds_exact(const int8_t* a, const void* w, const float* sa, const void* sw,
                           void* out, int32_t* ws, int m, int n, int k, hipStream_t stream) {
   auto kernel = channel_gemm_wlds_kernel<C, kCode, kWorkspace, kExactK>;
-  static bool configured = false;  // benign race: every thread sets the same attribute
-  if (!configured) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             C::kLdsBytes);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
+  static std::atomic<bool> configured{false};
+  if (const hipError_t e = raise_lds_limit_once(kernel, C::kLdsBytes, configured); e != hipSuccess)
+    return e;
   const int blocks = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
   const bool vec_n = n % 4 == 0 && reinterpret_cast<uintptr_t>(sw) % 8 == 0 &&
                      reinterpret_cast<uintptr_t>(out) % 8 == 0 &&
@@ -1080,14 +1070,9 @@ template <class C, WeightCode kCode, bool kWorkspace, bool kExactK>
 hipError_t run_k128_exact(const int8_t* a, const void* w, const float* sa, const void* sw,
                           void* out, int32_t* ws, int m, int n, int k, hipStream_t stream) {
   auto kernel = channel_gemm_k128_kernel<C, kCode, kWorkspace, kExactK>;
-  static bool configured = false;  // benign race: every thread sets the same attribute
-  if (!configured) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             C::kLdsBytes);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
+  static std::atomic<bool> configured{false};
+  if (const hipError_t e = raise_lds_limit_once(kernel, C::kLdsBytes, configured); e != hipSuccess)
+    return e;
   const int blocks = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
   const bool vec_n = n % 4 == 0 && reinterpret_cast<uintptr_t>(sw) % 8 == 0 &&
                      reinterpret_cast<uintptr_t>(out) % 8 == 0 &&
@@ -1250,14 +1235,9 @@ template <class C>
 hipError_t run_grouped(const int8_t* a, const int8_t* w, const float* sa, const void* sw,
                        void* out, int groups, int m, int n, int k, hipStream_t stream) {
   auto kernel = grouped_summed_kernel<C>;
-  static bool configured = false;  // benign race: every thread sets the same attribute
-  if (!configured) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             C::kLdsBytes);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
+  static std::atomic<bool> configured{false};
+  if (const hipError_t e = raise_lds_limit_once(kernel, C::kLdsBytes, configured); e != hipSuccess)
+    return e;
   const int blocks = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
   const bool vec_n = n % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0;
   kernel<<<blocks, C::kThreads, C::kLdsBytes, stream>>>(

@@ -369,13 +369,10 @@ hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale
   if (lds <= 72 * 1024) {  // plus 8 KiB of static LDS: two workgroups per CU
     using R = ResidentConfig<8, 10, 8>;
     auto kernel = channel_gemv_resident_kernel<R>;
-    static bool configured = false;  // benign race: every thread sets the same attribute
-    if (!configured && lds > 56 * 1024) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               72 * 1024);
-      if (e != hipSuccess) return e;
-      configured = true;
+    static std::atomic<bool> configured{false};
+    if (lds > 56 * 1024) {
+      if (const hipError_t e = raise_lds_limit_once(kernel, 72 * 1024, configured); e != hipSuccess)
+        return e;
     }
     const int grid = (n + 15) / 16;
     kernel<<<grid, R::kThreads, lds, stream>>>(
