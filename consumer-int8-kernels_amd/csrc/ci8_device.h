@@ -108,5 +108,10 @@ constexpr int vmcnt_imm(int n) {
 }
 // s_waitcnt immediate that waits for all LDS/scalar operations (lgkmcnt = 0).
 constexpr int lgkmcnt0_imm() { return 0xF | (0x3 << 14) | (0x7 << 4); }
+// s_waitcnt immediate for at most `vm` vector-memory and `lgkm` LDS/scalar operations
+// outstanding (lgkm <= 15).
+constexpr int vm_lgkm_imm(int vm, int lgkm) {
+  return (vm & 0xF) | ((vm >> 4) << 14) | (0x7 << 4) | ((lgkm & 0xF) << 8);
+}
 
 }  // namespace ci8

@@ -22,6 +22,7 @@
 //    the same XCD (the hardware deals workgroups round-robin over the 8 XCDs), which
 //    keeps the A and W panels they share in that XCD's L2.
 #include <type_traits>
+#include <utility>
 
 #include "ci8_device.h"
 #include "launch.h"
@@ -499,6 +500,32 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint
                                                int soffset) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voffset, soffset, 0));
 }
+// XOR `mask` into the 16 bytes at LDS byte address `addr + kOff`.
+template <int kOff>
+__device__ __forceinline__ void xor_16(uint32_t addr, uint64_t mask) {
+  static_assert(kOff >= 0 && kOff + 8 < 65536, "ds offset field");
+  asm volatile("ds_xor_b64 %0, %1 offset:%2\n\tds_xor_b64 %0, %1 offset:%3"
+               :
+               : "v"(addr), "v"(mask), "i"(kOff), "i"(kOff + 8)
+               : "memory");
+}
+// XOR 0x80 into every byte of the 16 bytes at LDS byte address
+// wave_base + 16 * lane + i * kStride, for each i in the sequence. The lane address and
+// the mask are made here, by volatile assembly the compiler cannot hoist, so that in a
+// loop they hold VGPRs only for these few instructions.
+template <int kStride, int... I>
+__device__ __forceinline__ void xor80_blocks(uint32_t wave_base, std::integer_sequence<int, I...>) {
+  uint32_t addr;
+  uint64_t mask;
+  asm volatile(
+      "v_mbcnt_lo_u32_b32 %0, -1, 0\n\t"
+      "v_mbcnt_hi_u32_b32 %0, -1, %0\n\t"
+      "v_lshl_add_u32 %0, %0, 4, %1"
+      : "=v"(addr)
+      : "s"(wave_base));
+  asm volatile("v_mov_b64 %0, %1" : "=v"(mask) : "s"(0x8080808080808080ull));
+  (xor_16<I * kStride>(addr, mask), ...);
+}
 template <int kImm>
 __device__ __forceinline__ void waitcnt() {
   __builtin_amdgcn_s_waitcnt(kImm);
@@ -899,38 +926,58 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
       }
     }
   };
+  // Biased UINT8 weights are debiased in LDS, once per stage: each wave XORs the kLoads
+  // 1 KiB blocks its own copies wrote with 0x80 in every byte (ds_xor_b64, 14 per lane
+  // for BN = 224), after those copies landed and before the barrier that hands the
+  // stage to the other waves. Debiasing the fragments in VGPRs instead would cost every
+  // wave one v_xor_b32 per fragment dword per K-step, four times the work, and the
+  // registers to hold it. Zero bytes from out-of-range copies become -128 codes; they
+  // meet zero A bytes (K padding) or feed output columns that are never stored.
+  // The XORs are inline assembly: the compiler would otherwise order them after every
+  // outstanding LDS copy (s_waitcnt vmcnt(0)), draining the A and W pipelines each
+  // stage. The explicit waits below order them instead; they are not counted in the
+  // compiler's own LDS waits, which can only make those waits stricter.
+  auto debias_w = [&] __device__(int t) __attribute__((always_inline)) {
+    if constexpr (kCode == WeightCode::kBiasedU8) {
+      const uint32_t wave_base = uint32_t(reinterpret_cast<uintptr_t>(
+          lds + (t & (C::kSlots - 1)) * C::kStageBytes + wave * 1024));
+      xor80_blocks<C::kWaves * 1024>(wave_base, std::make_integer_sequence<int, C::kLoads>{});
+    }
+  };
 
   // A loads: block j, K-step h -> 16 bytes of row (lane % 16) at chunk 2 * (lane / 16) + h.
   const int frag_row = lane & 15;
   const int frag_group = lane >> 4;
   const int a_row0 = m0 + wave * (C::BM / C::kWaves) + frag_row;
-  // Per-lane voffsets (the stage's K offset goes in the scalar soffset); rows past m
-  // start out of range and stay out of range whatever soffset is added.
-  uint32_t a_voff[C::TM][2];
+  // Per-lane voffsets of K-step 0 (the stage's K offset, and K-step 1's extra 16 bytes,
+  // go in the scalar soffset, so the two K-steps share one VGPR per block); rows past m
+  // start out of range and stay out of range whatever soffset is added. With K a
+  // multiple of 32, a lane's two 16-byte chunks of a stage are both in range or both
+  // past K.
+  uint32_t a_voff[C::TM];
 #pragma unroll
   for (int j = 0; j < C::TM; ++j) {
     const int row = a_row0 + j * 16;
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      a_voff[j][h] = row < m ? uint32_t(row) * uint32_t(k) + uint32_t(frag_group * 32 + h * 16)
-                             : kOutOfRange;
+    a_voff[j] = row < m ? uint32_t(row) * uint32_t(k) + uint32_t(frag_group * 32) : kOutOfRange;
   }
   i32x4 af[3][2][C::TM];  // [register set][K-step][m block]
   auto load_a = [&] __device__(int t, int set) __attribute__((always_inline)) {
     const int st = t < ns ? t : 0;
     const int k0 = st * C::BK;
 #pragma unroll
-    for (int j = 0; j < C::TM; ++j)
+    for (int j = 0; j < C::TM; ++j) {
+      if constexpr (kExactK) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if constexpr (kExactK) {
-          af[set][h][j] = __builtin_bit_cast(i32x4, buffer_load16(a_rsrc, a_voff[j][h], k0));
-        } else {
-          const bool live = a_voff[j][h] != kOutOfRange && k0 + frag_group * 32 + h * 16 < k;
-          af[set][h][j] = __builtin_bit_cast(
-              i32x4, buffer_load16(a_rsrc, live ? a_voff[j][h] + uint32_t(k0) : kOutOfRange, 0));
-        }
+        for (int h = 0; h < 2; ++h)
+          af[set][h][j] = __builtin_bit_cast(i32x4, buffer_load16(a_rsrc, a_voff[j], k0 + h * 16));
+      } else {
+        const bool live = a_voff[j] != kOutOfRange && k0 + frag_group * 32 < k;
+        const uint32_t voff = live ? a_voff[j] + uint32_t(k0) : kOutOfRange;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          af[set][h][j] = __builtin_bit_cast(i32x4, buffer_load16(a_rsrc, voff, h * 16));
       }
+    }
   };
 
   // W fragments: row (lane % 16) of each 16-row block, chunk 2 * (lane / 16) + h; the
@@ -954,10 +1001,8 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
   auto kstep = [&] __device__(int set, int h, int nt, int nh) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < C::TN; ++i) {
-      i32x4 x = xf[i];
-      if constexpr (kCode == WeightCode::kBiasedU8) x ^= int32_t(0x80808080u);
 #pragma unroll
-      for (int j = 0; j < C::TM; ++j) acc[j][i] = mfma16(x, af[set][h][j], acc[j][i]);
+      for (int j = 0; j < C::TM; ++j) acc[j][i] = mfma16(xf[i], af[set][h][j], acc[j][i]);
       xf[i] = ld(xaddr(nt, nh, i));
     }
   };
@@ -984,14 +1029,26 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
   // are counted in issue order: ..., A(t+1), W(t+2), A(t+2), so with the W copies of
   // stage t+1 issued before A(t+1) (stage t-1 issues A(t+1) then W(t+2); the prologue
   // issues W0 A0 W1 A1 W2 so t = 0 follows the same pattern), allowing A(t+1), W(t+2)
-  // and A(t+2) outstanding guarantees W(t+1).
+  // and A(t+2) outstanding guarantees W(t+1). With biased weights, own XORs of stage
+  // t+1 (issued at the start of stage t) completed too: LDS operations complete in
+  // order, and only the TN fragment reloads of K-step (t, 1) follow them.
+  static_assert(C::TN <= 15, "lgkmcnt field");
   auto sync = [&] __device__() __attribute__((always_inline)) {
-    waitcnt<vmcnt_imm((C::kAhead - 2) * C::kLoads + 4 * C::TM)>();
+    constexpr int kVm = (C::kAhead - 2) * C::kLoads + 4 * C::TM;
+    if constexpr (kCode == WeightCode::kBiasedU8)
+      waitcnt<vm_lgkm_imm(kVm, C::TN)>();
+    else
+      waitcnt<vmcnt_imm(kVm)>();
     workgroup_barrier();
   };
   // A is loaded two stages ahead into three register sets (set = stage % 3): the loads
-  // of stage t+2 go into the set stage t-1 used.
+  // of stage t+2 go into the set stage t-1 used. Biased weights: before those loads,
+  // wait for own W copies of stage t+1 (outstanding: A(t+1), W(t+2)) and debias them.
   auto stage = [&] __device__(int t, int set) __attribute__((always_inline)) {
+    if constexpr (kCode == WeightCode::kBiasedU8) {
+      waitcnt<vmcnt_imm((C::kAhead - 2) * C::kLoads + 2 * C::TM)>();
+      debias_w(t + 1);
+    }
     load_a(t + 2, (set + 2) % 3);
     kstep(set, 0, t, 1);
     sched_kstep(std::integral_constant<int, 0x020>{}, std::integral_constant<int, 2 * C::TM>{});
@@ -1012,6 +1069,10 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
   __builtin_amdgcn_sched_barrier(0);
   issue_w(2);
   waitcnt<vmcnt_imm(2 * C::kLoads + 2 * C::TM)>();  // W(0) and A(0) landed
+  if constexpr (kCode == WeightCode::kBiasedU8) {
+    debias_w(0);
+    __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+  }
   workgroup_barrier();
 #pragma unroll
   for (int i = 0; i < C::TN; ++i) xf[i] = ld(xaddr(0, 0, i));

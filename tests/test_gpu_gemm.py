@@ -57,7 +57,11 @@ def test_gemm_schedules_match_integer_products_and_capture(ops, m, fused, n, k):
     assert np.array_equal(bf16_bits(out), expected)
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 5120, 5120), (4, 2560, 3072), (17, 37, 128)])
+@pytest.mark.parametrize("m,n,k", [(1, 5120, 5120), (4, 2560, 3072), (17, 37, 128),
+                                   # M >= 1024: the large-tile kernel, which debiases each
+                                   # K stage in LDS; one stage, ragged K, partial tiles
+                                   (1024, 224, 128), (1041, 232, 544), (2057, 480, 4096),
+                                   (1100, 17, 96), (3000, 452, 1440)])
 def test_channel_mm_matches_integer_product_with_output_tails(ops, m, n, k):
     rng = np.random.default_rng(17)
     a_np, w_np, sa_np, sw_np = gemm_inputs(rng, m, n, k, biased=True)
