@@ -1031,12 +1031,13 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
   // issues W0 A0 W1 A1 W2 so t = 0 follows the same pattern), allowing A(t+1), W(t+2)
   // and A(t+2) outstanding guarantees W(t+1). With biased weights, own XORs of stage
   // t+1 (issued at the start of stage t) completed too: LDS operations complete in
-  // order, and only the TN fragment reloads of K-step (t, 1) follow them.
-  static_assert(C::TN <= 15, "lgkmcnt field");
+  // order, and only the TN fragment reloads of K-step (t, 1) follow them (the count
+  // field holds at most 15; a smaller count only waits longer).
   auto sync = [&] __device__() __attribute__((always_inline)) {
     constexpr int kVm = (C::kAhead - 2) * C::kLoads + 4 * C::TM;
+    constexpr int kLgkm = C::TN < 15 ? C::TN : 15;
     if constexpr (kCode == WeightCode::kBiasedU8)
-      waitcnt<vm_lgkm_imm(kVm, C::TN)>();
+      waitcnt<vm_lgkm_imm(kVm, kLgkm)>();
     else
       waitcnt<vmcnt_imm(kVm)>();
     workgroup_barrier();
@@ -1158,20 +1159,39 @@ using Medium = TileConfig<128, 128, 64, 2, 2, 3, 8>;  // 4 waves, 64x64 per wave
 using Small = TileConfig<256, 32, 128, 4, 1, 2, 1>;   // skinny M: 4 waves stacked on n
 using Pipe224 = K128Config<256, 224, 2, 2, 8>;        // 4 waves, 128x112 per wave
 using WLds224 = WLdsConfig<224, 8>;                   // 4 waves, 64x224 per wave
+using WLds256 = WLdsConfig<256, 8>;                   // 4 waves, 64x256 per wave
+
+// Whether 256-wide large tiles finish an m x n GEMM sooner than 224-wide ones. A launch
+// runs its tiles in rounds of one per CU, and a round takes time in proportion to the
+// tile width, so the cost of a width is rounds x width. 224 suits N = 17408 at M = 4096
+// (1,248 tiles, 4.9 rounds on 256 CUs, where 256-wide tiles need 4.25 rounds, i.e. 5);
+// 256 suits N = 5120 at M = 16384 (5 full rounds against 5.75).
+bool wide_tiles_pay(int m, int n) {
+  int device = 0, cus = 0;
+  if (hipGetDevice(&device) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      cus <= 0)
+    return false;
+  const int64_t tiles_m = (m + 255) / 256;
+  const int64_t rounds224 = (tiles_m * ((n + 223) / 224) + cus - 1) / cus;
+  const int64_t rounds256 = (tiles_m * ((n + 255) / 256) + cus - 1) / cus;
+  return rounds256 * 256 < rounds224 * 224;
+}
 
 template <WeightCode kCode, bool kWorkspace>
 hipError_t dispatch(const int8_t* a, const void* w, const float* sa, const void* sw, void* out,
                     int32_t* ws, int m, int n, int k, int schedule, hipStream_t stream) {
   int choice = schedule;
-  if (choice == 0) choice = m <= 32 ? 5 : (m < 1024 ? 1 : 4);
+  if (choice == 0) choice = m <= 32 ? 5 : (m < 1024 ? 1 : (wide_tiles_pay(m, n) ? 3 : 4));
   switch (choice) {
     case 5:
       return run<Small, kCode, kWorkspace>(a, w, sa, sw, out, ws, m, n, k, stream);
     case 1:
-    case 3:
       return run<Medium, kCode, kWorkspace>(a, w, sa, sw, out, ws, m, n, k, stream);
     case 2:
       return run<Large, kCode, kWorkspace>(a, w, sa, sw, out, ws, m, n, k, stream);
+    case 3:
+      return run_wlds<WLds256, kCode, kWorkspace>(a, w, sa, sw, out, ws, m, n, k, stream);
     default:
       return run_wlds<WLds224, kCode, kWorkspace>(a, w, sa, sw, out, ws, m, n, k, stream);
     case 6:

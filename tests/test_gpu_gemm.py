@@ -215,6 +215,35 @@ def test_down_projection_biased_weights_full_size(ops):
     full_size_check(a_np, w_signed, sa_np, sw_np, ws, out_bits, samples=8)
 
 
+@pytest.mark.parametrize("biased", [False, True])
+def test_wide_tiles_where_they_fill_the_rounds(ops, biased):
+    """M = N = 4096: 304 tiles of 256 x 224 need 2 rounds on 256 CUs and 256 tiles of
+    256 x 256 need 1, so schedule 0 (and channel_mm) runs the 256-wide kernel, with a
+    K that is not a whole number of 128-byte stages. It agrees bit for bit with the
+    128 x 128 tiling (schedule 1) and, through the exact INT32 accumulators of the
+    workspace variant, with the oracle on sampled rows and columns."""
+    m, n, k = 4096, 4096, 1056
+    rng = np.random.default_rng(256 + biased)
+    a_np, w_np, sa_np, sw_np = gemm_inputs(rng, m, n, k, biased=biased)
+    w_signed = O.debias(w_np) if biased else w_np
+    a, sa, sw, ws_dev = to_dev(a_np), to_dev(sa_np), to_dev(sw_np), to_dev(w_signed)
+    out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    if biased:
+        ops.channel_mm(a, to_dev(w_np), sa, sw, out)
+    else:
+        ops.fused_channel_mm(a, ws_dev, sa, sw, out, 0)
+    ref = torch.empty_like(out)
+    ops.fused_channel_mm(a, ws_dev, sa, sw, ref, 1)
+    acc = torch.empty(m, n, device="cuda", dtype=torch.int32)
+    out2 = torch.empty_like(out)
+    ops.cutlass_channel_mm(a, ws_dev, sa, sw, acc, out2)
+    torch.cuda.synchronize()
+    out_bits = bf16_bits(out)
+    assert np.array_equal(out_bits, bf16_bits(ref))
+    assert np.array_equal(out_bits, bf16_bits(out2))
+    full_size_check(a_np, w_signed, sa_np, sw_np, acc, out_bits, samples=8)
+
+
 def test_c_abi_fused_matches_oracle(ops, lib):
     from consumer_int8 import _abi
 
