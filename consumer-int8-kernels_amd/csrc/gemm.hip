@@ -526,6 +526,20 @@ __device__ __forceinline__ void xor80_blocks(uint32_t wave_base, std::integer_se
   asm volatile("v_mov_b64 %0, %1" : "=v"(mask) : "s"(0x8080808080808080ull));
   (xor_16<I * kStride>(addr, mask), ...);
 }
+// ds_write_b128 of v to LDS byte address addr + kOff. Inline assembly, for the same
+// reason as the XORs above: the compiler orders a plain LDS store after every
+// outstanding LDS copy.
+template <int kOff>
+__device__ __forceinline__ void ds_write16(uint32_t addr, u32x4 v) {
+  static_assert(kOff >= 0 && kOff < 65536, "ds offset field");
+  asm volatile("ds_write_b128 %0, %1 offset:%2" : : "v"(addr), "v"(v), "i"(kOff) : "memory");
+}
+// v[i] to addr + i * kStride for each i in the sequence.
+template <int kStride, int... I>
+__device__ __forceinline__ void ds_write_blocks(uint32_t addr, const u32x4* v,
+                                                std::integer_sequence<int, I...>) {
+  (ds_write16<I * kStride>(addr, v[I]), ...);
+}
 template <int kImm>
 __device__ __forceinline__ void waitcnt() {
   __builtin_amdgcn_s_waitcnt(kImm);
@@ -756,36 +770,42 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_k128_kernel(
 }
 
 // ---------------------------------------------------------------------------------
-// Large-tile kernel with W staged in LDS and A loaded straight into registers.
+// Large-tile kernel with W staged in a shared LDS ring and A private to each wave.
 //
-// Tile 256(m) x 224(n); the four waves are stacked along m, each owning 64 rows x 224
-// columns as 4 x 14 16x16 INT32 accumulators (224 AGPRs). A wave's A rows are private
-// to it, so they are loaded from L2 directly into the MFMA operand registers (no LDS,
-// no sharing, no extra traffic), while the 224 W rows, used by all four waves, go
-// through an LDS ring filled by buffer_load ... lds. With only W in LDS a stage of 128
-// K-bytes is 28 KB, so a ring of four slots keeps three stages in flight, and the A
-// loads of the next two stages are in flight in two more register sets (three sets in
-// all): about 124 KB of operands in flight per CU (twice what fits when both operands
-// share LDS). Measured with per-wave clocks on MI355X, the main loop is limited by the
-// vector-memory path (TA/L1) feeding the A loads, whose 16-row x 64-byte pattern moves
-// fewer bytes per cycle than whole-line copies; loading A two stages ahead instead of
-// one saves about 4% of the cycles per stage.
+// Tile 256(m) x 224(n) (or 256-wide); the four waves are stacked along m, each owning
+// 64 rows x 224 columns as 4 x 14 16x16 INT32 accumulators (224 AGPRs). The 224 W rows,
+// used by all four waves, go through an LDS ring filled by buffer_load ... lds. With only
+// W in LDS a stage of 128 K-bytes is 28 KB, so a ring of four slots keeps three stages in
+// flight. A wave's A rows are private to it; the A loads of the next two stages are in
+// flight in two more register sets (three sets in all). Measured with per-wave clocks on
+// MI355X, the main loop is limited by the vector-memory address unit (TA), and A is
+// the costly stream: loaded straight into MFMA operand registers, each load touches 16
+// rows x 64 bytes, which the unit serves at ~16 B/clk per CU, against ~26 B/clk for 8
+// rows x 128 bytes and ~55 B/clk for the W copies. So with the 224-wide tile and K a
+// whole number of stages, A takes a detour (kABounce): 8-row x 128-byte loads into
+// staging registers, then the wave's own 8 KiB LDS buffer, then fragment reads in the
+// operand layout. That is 4% faster at configs[2]; the 256-wide tile has no LDS left for
+// the buffers and loads A straight into the operand registers.
 //
 // K order: within a 128-byte stage, MFMA lane group g (lane / 16) takes physical chunk
 // 2g + h in K-step h (0 or 1). A and W use the same order, so the dot products are
-// unchanged, and each lane's two 16-byte A loads per block cover a whole 128-byte line
-// of its row.
+// unchanged, and each lane's two 16-byte direct A loads per block cover a whole
+// 128-byte line of its row.
 //
 // For stage t (K-steps h = 0, 1), each wave:
 //   h = 0: issue the A loads of stage t+2 (into the set stage t-1 used); 56 MFMAs;
-//          reload each W fragment for K-step (t, 1) right after its last MFMA;
-//   sync:  own W copies of stage t+1 landed, then a barrier (all waves' copies landed;
-//          every wave finished K-step (t, 0), so nobody reads the slot of stage t-1);
+//          reload each W fragment for K-step (t, 1) right after its last MFMA (bounce:
+//          and read the A fragments of K-step (t, 1) from the buffer);
+//   sync:  own W copies (bounce: and A loads) of stage t+1 landed, then a barrier (all
+//          waves' copies landed; every wave finished K-step (t, 0), so nobody reads the
+//          slot of stage t-1); bounce: write A of stage t+1 to the buffer, after the
+//          reads of stage t's fragments in program order;
 //   h = 1: issue the W copies of stage t+3 into the slot of stage t-1; 56 MFMAs;
-//          reload the W fragments for K-step (t+1, 0).
-template <int BN_, int GROUP_M_>
+//          reload the W fragments (bounce: and read the A fragments) for K-step (t+1, 0).
+template <int BN_, int GROUP_M_, bool kABounce_>
 struct WLdsConfig {
   static constexpr int BM = 256, BN = BN_, GROUP_M = GROUP_M_;
+  static constexpr bool kABounce = kABounce_;  // A through a per-wave LDS buffer
   static constexpr int BK = 128;        // K bytes per stage (two 64-deep MFMA steps)
   static constexpr int kWaves = 4;      // stacked along m
   static constexpr int kThreads = 256;
@@ -803,8 +823,13 @@ struct WLdsConfig {
   // ds_write_b64 covers start in distinct banks).
   static constexpr int kEpiRowBytes = BN * 2 + 16;
   static constexpr int kEpiWaveBytes = (BM / kWaves) * kEpiRowBytes;
+  // A bounce buffers: one per wave, its 64 rows x 128 bytes of a stage, after the ring.
+  static constexpr int kABytes = (BM / kWaves) * BK;
+  static constexpr int kABase = kRingBytes;
+  static constexpr int kMainBytes = kRingBytes + (kABounce ? kWaves * kABytes : 0);
   static constexpr int kLdsBytes =
-      kRingBytes > kWaves * kEpiWaveBytes ? kRingBytes : kWaves * kEpiWaveBytes;
+      kMainBytes > kWaves * kEpiWaveBytes ? kMainBytes : kWaves * kEpiWaveBytes;
+  static constexpr int kALoads = kABounce ? BM / kWaves / 8 : 2 * TM;  // A loads per stage
   static_assert(kLoads * kWaves == kBlocks, "whole 1 KiB W blocks per wave");
   static_assert((BN * 2) % 16 == 0, "whole 16-byte output chunks per row");
   static_assert(TM * 16 * kWaves == BM && TN * 16 == BN, "wave tiling");
@@ -945,38 +970,73 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
     }
   };
 
-  // A loads: block j, K-step h -> 16 bytes of row (lane % 16) at chunk 2 * (lane / 16) + h.
+  constexpr bool kBounce = C::kABounce && kExactK;
   const int frag_row = lane & 15;
   const int frag_group = lane >> 4;
-  const int a_row0 = m0 + wave * (C::BM / C::kWaves) + frag_row;
-  // Per-lane voffsets of K-step 0 (the stage's K offset, and K-step 1's extra 16 bytes,
-  // go in the scalar soffset, so the two K-steps share one VGPR per block); rows past m
-  // start out of range and stay out of range whatever soffset is added. With K a
-  // multiple of 32, a lane's two 16-byte chunks of a stage are both in range or both
-  // past K.
-  uint32_t a_voff[C::TM];
+  // A operand, K-step h of block j: 16 bytes of row (lane % 16) at chunk
+  // 2 * (lane / 16) + h. Two ways to get it there, both loading stage t+2 at the start
+  // of stage t into register set (t+2) % 3 (the bounce only where K is a whole number of
+  // stages: with the per-load K-tail checks it no longer fits in registers):
+  //  * direct (kABounce false): each lane loads its own fragments, 16 rows x 64 bytes
+  //    per load, which the vector-memory address unit serves at ~16 B/clk per CU;
+  //  * bounce (kABounce true): loads of 8 rows x 128 bytes (lane: row lane / 8, chunk
+  //    lane % 8; ~26 B/clk per CU) into staging registers, written at the middle of
+  //    stage t-1 to this wave's own LDS buffer (chunks XOR-swizzled by row % 8) and read
+  //    back as fragments one K-step ahead. The buffer is private to the wave, whose LDS
+  //    operations complete in order, so it needs no barrier.
+  // Per-lane voffsets carry the row (the stage's K offset goes in the scalar soffset);
+  // rows past m start out of range and stay out of range whatever soffset is added.
+  // With K a multiple of 32, a lane's 16- or 32-byte piece of a stage is wholly in range
+  // or wholly past K.
+  constexpr int kAOff = kBounce ? 8 : C::TM;
+  const int a_lrow = kBounce ? (lane >> 3) : frag_row;     // row within a load
+  const int a_lcol = kBounce ? (lane & 7) * 16 : frag_group * 32;  // byte within a stage
+  const int a_rstep = kBounce ? 8 : 16;                   // rows between loads
+  uint32_t a_voff[kAOff];
 #pragma unroll
-  for (int j = 0; j < C::TM; ++j) {
-    const int row = a_row0 + j * 16;
-    a_voff[j] = row < m ? uint32_t(row) * uint32_t(k) + uint32_t(frag_group * 32) : kOutOfRange;
+  for (int q = 0; q < kAOff; ++q) {
+    const int row = m0 + wave * (C::BM / C::kWaves) + q * a_rstep + a_lrow;
+    a_voff[q] = row < m ? uint32_t(row) * uint32_t(k) + uint32_t(a_lcol) : kOutOfRange;
   }
-  i32x4 af[3][2][C::TM];  // [register set][K-step][m block]
+  i32x4 af[kBounce ? 1 : 3][2][C::TM];  // [register set][K-step][m block]
+  u32x4 as[kBounce ? 3 : 1][8];          // bounce staging [register set][load]
   auto load_a = [&] __device__(int t, int set) __attribute__((always_inline)) {
     const int st = t < ns ? t : 0;
     const int k0 = st * C::BK;
 #pragma unroll
-    for (int j = 0; j < C::TM; ++j) {
-      if constexpr (kExactK) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          af[set][h][j] = __builtin_bit_cast(i32x4, buffer_load16(a_rsrc, a_voff[j], k0 + h * 16));
-      } else {
-        const bool live = a_voff[j] != kOutOfRange && k0 + frag_group * 32 < k;
-        const uint32_t voff = live ? a_voff[j] + uint32_t(k0) : kOutOfRange;
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          af[set][h][j] = __builtin_bit_cast(i32x4, buffer_load16(a_rsrc, voff, h * 16));
+    for (int q = 0; q < kAOff; ++q) {
+      uint32_t voff = a_voff[q];
+      int soff = k0;
+      if constexpr (!kExactK) {
+        voff = voff != kOutOfRange && k0 + a_lcol < k ? voff + uint32_t(k0) : kOutOfRange;
+        soff = 0;
       }
+      if constexpr (kBounce) {
+        as[set][q] = buffer_load16(a_rsrc, voff, soff);
+      } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          af[set][h][q] = __builtin_bit_cast(i32x4, buffer_load16(a_rsrc, voff, soff + h * 16));
+      }
+    }
+  };
+  auto* a_buf = lds + C::kABase + wave * C::kABytes;
+  const uint32_t a_wr = uint32_t(reinterpret_cast<uintptr_t>(a_buf)) +
+                        uint32_t(a_lrow * C::BK + (((lane & 7) ^ a_lrow) * 16));
+  auto store_a = [&] __device__(int set) __attribute__((always_inline)) {
+    if constexpr (kBounce)
+      ds_write_blocks<8 * C::BK>(a_wr, as[set], std::make_integer_sequence<int, 8>{});
+  };
+  int a_rd[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    a_rd[h] = frag_row * C::BK + (((2 * frag_group + h) ^ (frag_row & 7)) * 16);
+  auto read_a = [&] __device__(int h) __attribute__((always_inline)) {
+    if constexpr (kBounce) {
+#pragma unroll
+      for (int j = 0; j < C::TM; ++j)
+        af[0][h][j] = *reinterpret_cast<const __attribute__((address_space(3))) i32x4*>(
+            a_buf + a_rd[h] + j * 16 * C::BK);
     }
   };
 
@@ -1002,8 +1062,10 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
 #pragma unroll
     for (int i = 0; i < C::TN; ++i) {
 #pragma unroll
-      for (int j = 0; j < C::TM; ++j) acc[j][i] = mfma16(xf[i], af[set][h][j], acc[j][i]);
+      for (int j = 0; j < C::TM; ++j)
+        acc[j][i] = mfma16(xf[i], af[kBounce ? 0 : set][h][j], acc[j][i]);
       xf[i] = ld(xaddr(nt, nh, i));
+      if (i == 0) read_a(nh);  // bounce: the A fragments of K-step (nt, nh)
     }
   };
   // Scheduling: the K-step's VMEM instructions alternate with its first MFMAs (which
@@ -1018,24 +1080,27 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
       sched_group<decltype(vmem_mask)::value, 1>();
     }
     if constexpr (2 * C::TM > kVmem) sched_group<0x008, 2 * C::TM - kVmem>();
-    sched_group<0x100, 2>();  // W fragments 0, 1
+    sched_group<0x100, 2 + (kBounce ? C::TM : 0)>();  // W fragments 0, 1 (and A's)
 #pragma unroll
     for (int i = 2; i < C::TN; ++i) {
       sched_group<0x008, C::TM>();
       sched_group<0x100, 1>();
     }
   };
-  // Before K-step (t, 1): own W copies of stage t+1 landed. Vector-memory operations
-  // are counted in issue order: ..., A(t+1), W(t+2), A(t+2), so with the W copies of
-  // stage t+1 issued before A(t+1) (stage t-1 issues A(t+1) then W(t+2); the prologue
-  // issues W0 A0 W1 A1 W2 so t = 0 follows the same pattern), allowing A(t+1), W(t+2)
-  // and A(t+2) outstanding guarantees W(t+1). With biased weights, own XORs of stage
-  // t+1 (issued at the start of stage t) completed too: LDS operations complete in
-  // order, and only the TN fragment reloads of K-step (t, 1) follow them (the count
-  // field holds at most 15; a smaller count only waits longer).
+  // Before K-step (t, 1): own W copies of stage t+1 landed (and, for the A bounce,
+  // own A loads of stage t+1, which go to the LDS buffer right after the barrier).
+  // Vector-memory operations are counted in issue order: ..., W(t+1), A(t+1), W(t+2),
+  // A(t+2) (stage t-1 issues A(t+1) then W(t+2); the prologue issues W0 A0 W1 A1 W2 so
+  // t = 0 follows the same pattern). Allowing A(t+1), W(t+2) and A(t+2) outstanding
+  // guarantees W(t+1); allowing only W(t+2) and A(t+2) also guarantees A(t+1). With
+  // biased weights, own XORs of stage t+1 (issued at the start of stage t) completed
+  // too: LDS operations complete in order, and only the TN W (and, bounce, TM A)
+  // fragment reads of K-step (t, 1) follow them (the count field holds at most 15; a
+  // smaller count only waits longer).
   auto sync = [&] __device__() __attribute__((always_inline)) {
-    constexpr int kVm = (C::kAhead - 2) * C::kLoads + 4 * C::TM;
-    constexpr int kLgkm = C::TN < 15 ? C::TN : 15;
+    constexpr int kVm = (C::kAhead - 2) * C::kLoads + (kBounce ? 1 : 2) * C::kALoads;
+    constexpr int kDs = C::TN + (kBounce ? C::TM : 0);
+    constexpr int kLgkm = kDs < 15 ? kDs : 15;
     if constexpr (kCode == WeightCode::kBiasedU8)
       waitcnt<vm_lgkm_imm(kVm, kLgkm)>();
     else
@@ -1047,13 +1112,14 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
   // wait for own W copies of stage t+1 (outstanding: A(t+1), W(t+2)) and debias them.
   auto stage = [&] __device__(int t, int set) __attribute__((always_inline)) {
     if constexpr (kCode == WeightCode::kBiasedU8) {
-      waitcnt<vmcnt_imm((C::kAhead - 2) * C::kLoads + 2 * C::TM)>();
+      waitcnt<vmcnt_imm((C::kAhead - 2) * C::kLoads + C::kALoads)>();
       debias_w(t + 1);
     }
     load_a(t + 2, (set + 2) % 3);
     kstep(set, 0, t, 1);
-    sched_kstep(std::integral_constant<int, 0x020>{}, std::integral_constant<int, 2 * C::TM>{});
+    sched_kstep(std::integral_constant<int, 0x020>{}, std::integral_constant<int, C::kALoads>{});
     sync();
+    store_a((set + 1) % 3);  // bounce: A of stage t+1 into the wave's LDS buffer
     issue_w(t + C::kAhead);
     kstep(set, 1, t + 1, 0);
     sched_kstep(std::integral_constant<int, 0x010>{}, std::integral_constant<int, C::kLoads>{});
@@ -1069,7 +1135,9 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
   load_a(1, 1);
   __builtin_amdgcn_sched_barrier(0);
   issue_w(2);
-  waitcnt<vmcnt_imm(2 * C::kLoads + 2 * C::TM)>();  // W(0) and A(0) landed
+  __builtin_amdgcn_sched_barrier(0);
+  waitcnt<vmcnt_imm(2 * C::kLoads + C::kALoads)>();  // W(0) and A(0) landed
+  store_a(0);
   if constexpr (kCode == WeightCode::kBiasedU8) {
     debias_w(0);
     __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
@@ -1077,6 +1145,7 @@ __global__ void __launch_bounds__(C::kThreads, 1) channel_gemm_wlds_kernel(
   workgroup_barrier();
 #pragma unroll
   for (int i = 0; i < C::TN; ++i) xf[i] = ld(xaddr(0, 0, i));
+  read_a(0);
 
   int t = 0;
   for (; t + 2 < ns; t += 3) {
@@ -1158,8 +1227,8 @@ using Large = TileConfig<256, 256, 64, 2, 2, 3, 8>;   // 4 waves, 128x128 per wa
 using Medium = TileConfig<128, 128, 64, 2, 2, 3, 8>;  // 4 waves, 64x64 per wave
 using Small = TileConfig<256, 32, 128, 4, 1, 2, 1>;   // skinny M: 4 waves stacked on n
 using Pipe224 = K128Config<256, 224, 2, 2, 8>;        // 4 waves, 128x112 per wave
-using WLds224 = WLdsConfig<224, 8>;                   // 4 waves, 64x224 per wave
-using WLds256 = WLdsConfig<256, 8>;                   // 4 waves, 64x256 per wave
+using WLds224 = WLdsConfig<224, 8, true>;             // 4 waves, 64x224 per wave
+using WLds256 = WLdsConfig<256, 8, false>;            // 4 waves, 64x256 per wave
 
 // Whether 256-wide large tiles finish an m x n GEMM sooner than 224-wide ones. A launch
 // runs its tiles in rounds of one per CU, and a round takes time in proportion to the
