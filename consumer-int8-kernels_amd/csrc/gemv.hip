@@ -27,10 +27,11 @@
 //  * One barrier per stage. The ring has three slots, held in three separate LDS
 //    arrays so the compiler can see that the slot being read is not the slot an
 //    in-flight copy is writing.
-// For small batches (x[0:m, :] within 72 KiB of LDS: m <= 6 at K = 5120) a second kernel
+// For small batches (x[0:m, :] within 64 KiB of LDS: m <= 6 at K = 5120) a second kernel
 // copies all of x into LDS once and then lets every wave stream its W through a rolling
 // window of ten 64-byte blocks with no barriers at all, which removes the per-stage
-// lock-step of the ring.
+// lock-step of the ring. Up to 160 KiB of LDS (m <= 14 at K = 5120), a persistent form
+// of it runs one workgroup per CU that copies x once and walks its channel blocks.
 // Weight rows past N and K chunks past K read as zero through the buffer range check.
 #include "ci8_device.h"
 #include "launch.h"
@@ -356,6 +357,127 @@ __global__ void __launch_bounds__(C::kThreads, C::kWavesPerEU) channel_gemv_resi
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Persistent variant of the resident kernel, for batches whose x fills half the LDS or
+// more (one workgroup per CU, so it runs 16 waves, one per K range). Copying x per block of 16 channels would then cost each
+// CU a serial x copy per block; here each workgroup copies x once and walks the channel
+// blocks blockIdx.x, blockIdx.x + gridDim.x, ... Each wave's W window runs across block
+// boundaries: slot f of the flattened sequence (local block f / spb, K slot f % spb, spb
+// = the padded slots per block) is refilled with slot f + kAhead, so the loads of the
+// next block are in flight while a block's partial sums are reduced. The per-block
+// arithmetic and summation order are those of the resident kernel, so the bits are too.
+template <class C>
+__global__ void __launch_bounds__(C::kThreads, C::kWavesPerEU) channel_gemv_persistent_kernel(
+    const uint16_t* __restrict__ x, const int8_t* __restrict__ w,
+    const uint16_t* __restrict__ scale, uint16_t* __restrict__ out, int m, int n, int k) {
+  extern __shared__ __attribute__((aligned(1024))) char xs_raw[];
+  __shared__ f32x4 partial[C::kS][64];
+  const lds_char* xs = (const lds_char*)xs_raw;
+
+  const int lane = threadIdx.x & 63;
+  const int range = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row = lane & 15, group = lane >> 4;
+  const int nblocks = (n + 15) / 16;
+  const int nlocal = (nblocks - int(blockIdx.x) + int(gridDim.x) - 1) / int(gridDim.x);
+
+  const auto w_rsrc = make_rsrc(w, uint32_t(n) * uint32_t(k));
+  const auto x_rsrc = make_rsrc(x, uint32_t(m) * uint32_t(k) * 2u);
+  const auto s_rsrc = make_rsrc(scale, uint32_t(n) * 2u);
+  const int kblocks = (k + 63) / 64;
+  const int range_len = (kblocks + C::kS - 1) / C::kS;
+  const int kb_first = range * range_len;
+  const int kend = min(kb_first + range_len, kblocks);
+  const int groups = (range_len + C::kAhead - 1) / C::kAhead;
+  const int spb = groups * C::kAhead;  // slots per block (wave-uniform)
+
+  // Lane offset of W for local block lb; channels past N re-read row N-1 (their outputs
+  // are never stored).
+  auto w_lane = [&] __device__(int lb) __attribute__((always_inline)) {
+    const int channel = (int(blockIdx.x) + lb * int(gridDim.x)) * 16 + row;
+    return uint32_t(min(channel, n - 1)) * uint32_t(k) + uint32_t(group * 16);
+  };
+  auto w_offset = [&] __device__(int f) __attribute__((always_inline)) {
+    const int lb = f / spb;
+    const int kb = kb_first + (f - lb * spb);
+    return lb < nlocal && kb < kend ? w_lane(lb) + uint32_t(kb * 64) : kOutOfRange;
+  };
+  auto scale_bits = [&] __device__(int lb) __attribute__((always_inline)) {
+    const int channel = (int(blockIdx.x) + lb * int(gridDim.x)) * 16 + row;
+    return __builtin_amdgcn_raw_buffer_load_b16(
+        s_rsrc, lb < nlocal ? uint32_t(channel) * 2u : kOutOfRange, 0, 0);
+  };
+
+  // x copy, as in the resident kernel.
+  const int row_units = kblocks * 8;
+  const int units = m * row_units;
+  for (int u0 = range * 64; u0 < units; u0 += C::kThreads) {
+    const int u = u0 + lane;
+    const int r = u / row_units, within = u % row_units;
+    const int kb = within >> 3, c = (within & 7) ^ (r & 7);
+    const bool valid = u < units && kb * 64 + c * 8 < k;
+    copy16(x_rsrc, reinterpret_cast<lds_void*>((lds_char*)xs_raw + u0 * 16),
+           valid ? uint32_t(r) * uint32_t(k) * 2u + uint32_t(kb * 128 + c * 16) : kOutOfRange);
+  }
+  uint32_t s_next = scale_bits(0);
+  u32x4 wv[C::kAhead];
+#pragma unroll
+  for (int a = 0; a < C::kAhead; ++a) {
+    wv[a] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(a), 0, 0));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  waitcnt<vmcnt_imm(C::kAhead)>();  // the first scale and this wave's x copies have landed
+  workgroup_barrier();              // every wave's x copies have landed
+
+  const int xr = min(row, m - 1);
+  const lds_char* x_lane = xs + xr * kblocks * 128 + kb_first * 128;
+  const int swz0 = ((2 * group) ^ (xr & 7)) * 16, swz1 = ((2 * group + 1) ^ (xr & 7)) * 16;
+  for (int lb = 0; lb < nlocal; ++lb) {
+    const float s = bf16_to_f32(s_next);
+    s_next = scale_bits(lb + 1);  // in flight during this block
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int g = 0; g < groups; ++g) {
+#pragma unroll
+      for (int a = 0; a < C::kAhead; ++a) {
+        const int slot = g * C::kAhead + a;   // wave-uniform
+        const int kb = kb_first + slot;
+        waitcnt<vmcnt_imm(C::kAhead - 1)>();  // slot a's W has landed
+        if (kb < kend) {
+          const lds_char* xb = x_lane + slot * 128;
+          const u32x4 x0 = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xb + swz0);
+          const u32x4 x1 = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(xb + swz1);
+          const u32x4 wq = wv[a];
+          const u32x2 d0 = dequant4(wq[0], s), d1 = dequant4(wq[1], s);
+          const u32x2 d2 = dequant4(wq[2], s), d3 = dequant4(wq[3], s);
+          acc = mfma_bf16(u32x4{d0[0], d0[1], d1[0], d1[1]}, x0, acc);
+          acc = mfma_bf16(u32x4{d2[0], d2[1], d3[0], d3[1]}, x1, acc);
+        }
+        wv[a] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              w_rsrc, w_offset(lb * spb + slot + C::kAhead), 0, 0));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // Sum the K ranges' partials of this block in a fixed order; the barrier after the
+    // stores keeps the next block's partials from overwriting these early.
+    partial[range][lane] = acc;
+    __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+    workgroup_barrier();
+    const int block = int(blockIdx.x) + lb * int(gridDim.x);
+    for (int e_slot = threadIdx.x; e_slot < 64 * 4; e_slot += C::kThreads) {
+      const int e = e_slot & 3, l = e_slot >> 2;
+      const int out_row = l & 15;
+      const int out_col = block * 16 + (l >> 4) * 4 + e;
+      if (out_row >= m || out_col >= n) continue;
+      float sum = partial[0][l][e];
+#pragma unroll
+      for (int v = 1; v < C::kS; ++v) sum += partial[v][l][e];
+      out[int64_t(out_row) * n + out_col] = uint16_t(f32_to_bf16(sum));
+    }
+    __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+    workgroup_barrier();
+  }
+  waitcnt<vmcnt_imm(0)>();  // drain the trailing (out-of-range) loads before exit
+}
+
 }  // namespace
 
 hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale, void* out,
@@ -366,7 +488,9 @@ hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale
   // (m = 8: 30.5 against 26.2 us) the ring with 2 channel blocks x 2 K ranges and
   // 4-block stages is faster.
   const int lds = resident_lds_bytes(m, k);
-  if (lds <= 72 * 1024) {  // plus 8 KiB of static LDS: two workgroups per CU
+  // At m = 7 (71 KiB) the resident kernel still fits twice per CU but measures slower
+  // than the persistent one (25.7 against 24.6 us at m = 8), so it stops at 64 KiB.
+  if (lds <= 64 * 1024) {  // plus 8 KiB of static LDS: two workgroups per CU
     using R = ResidentConfig<8, 10, 8>;
     auto kernel = channel_gemv_resident_kernel<R>;
     static std::atomic<bool> configured{false};
@@ -376,6 +500,27 @@ hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale
     }
     const int grid = (n + 15) / 16;
     kernel<<<grid, R::kThreads, lds, stream>>>(
+        static_cast<const uint16_t*>(x), w, static_cast<const uint16_t*>(scale),
+        static_cast<uint16_t*>(out), m, n, k);
+    return hipGetLastError();
+  }
+  // Larger batches while x still fits (m = 7 .. 14 at K = 5120): the persistent kernel,
+  // one 16-wave workgroup per CU copying x once, with 5-block windows (at m = 8, 10,
+  // 14: 24.2 - 25.0 us, against 28 - 29 us with 8 waves and 16-block windows, and
+  // 26 - 27 us for the ring).
+  using P = ResidentConfig<16, 5, 4>;
+  constexpr int kStaticLds = P::kS * 64 * 16;  // partial sums
+  int device = 0, cus = 0;
+  if (lds + kStaticLds <= 160 * 1024 && hipGetDevice(&device) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess &&
+      cus > 0) {
+    auto kernel = channel_gemv_persistent_kernel<P>;
+    static std::atomic<bool> configured{false};
+    if (const hipError_t e = raise_lds_limit_once(kernel, 160 * 1024 - kStaticLds, configured);
+        e != hipSuccess)
+      return e;
+    const int grid = min((n + 15) / 16, cus);
+    kernel<<<grid, P::kThreads, lds, stream>>>(
         static_cast<const uint16_t*>(x), w, static_cast<const uint16_t*>(scale),
         static_cast<uint16_t*>(out), m, n, k);
     return hipGetLastError();

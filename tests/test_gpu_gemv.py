@@ -62,6 +62,23 @@ def test_decode_shape_full_size(ops, m):
     check_gemv(bf16_bits(out), x_bits, w, s_bits)
 
 
+@pytest.mark.parametrize("m,n,k", [(12, 1000, 5104), (10, 4100, 5120), (14, 250, 5120),
+                                   (9, 17, 8192), (10, 16 * 256 * 3 + 16, 5120),
+                                   (7, 300, 5120)])
+def test_persistent_batches_walk_their_channel_blocks(ops, m, n, k):
+    """Batches whose x takes more than 64 KiB of LDS (7 <= m <= 14 at K = 5120) run one
+    workgroup per CU that walks channel blocks blockIdx.x, blockIdx.x + grid, ...: fewer
+    blocks than CUs, more (unevenly shared), a partial last block and a K tail."""
+    rng = np.random.default_rng(m * 7 + n + k)
+    x_bits = randn_bf16(rng, (m, k))
+    w = rng.integers(-128, 128, (n, k)).astype(np.int8)
+    s_bits = O.f32_to_bf16(rng.uniform(1e-3, 1e-2, n).astype(np.float32))
+    out = torch.full((m, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+    ops.channel_gemv(to_dev(x_bits), to_dev(w), to_dev(s_bits), out)
+    torch.cuda.synchronize()
+    check_gemv(bf16_bits(out), x_bits, w, s_bits)
+
+
 @pytest.mark.parametrize("m,n,k", [(3, 100, 16), (5, 64, 48), (16, 7, 1040), (2, 33, 65536)])
 def test_gemv_tails_and_unaligned_activations(ops, m, n, k):
     rng = np.random.default_rng(m * n + k)
