@@ -22,7 +22,9 @@ host's cores.
 
 Before the W warm-up steps the same step runs untimed for `--condition-seconds` (0.15 s),
 because the chip ramps its clock over tens of milliseconds after idle; the count is
-reported as `conditioning`. The timed region is exactly K steps.
+reported as `conditioning`. The timed region is exactly K steps. The two other
+MFMA-bound extras (the grouped summed GEMM and the down projection) get 0.15 s of
+untimed launches of their own before they are timed.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-extras]
                       [--copy-calibration] [--condition-seconds S]
