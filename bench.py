@@ -17,8 +17,8 @@ GEMV, the grouped summed GEMM, the biased-UINT8 down
 projection with its SwiGLU activation producers (silu_mul_quantize,
 silu_mul) and the AllSpark weight restore (unpack_allspark), and the small quantize +
 GEMM pass (configs[0]); and
-`cpu_baseline`, the CPU oracle on a bounded row slice of the same workload on this
-host's cores.
+`cpu_baseline`, the reference's torch CPU math for the same step on a bounded row slice,
+on this host's cores.
 
 Before the W warm-up steps the same step runs untimed for `--condition-seconds` (0.15 s),
 because the chip ramps its clock over tens of milliseconds after idle; the count is
@@ -160,43 +160,67 @@ def mfma_clock_probe(torch, cus: int, rounds: int = 4000, reps: int = 5) -> dict
             "peak_at_clock_tops": round(cus * 8192 * clock * 1e6 / 1e12, 1)}
 
 
-def cpu_baseline(budget_s: float) -> dict:
-    """The CPU oracle (numpy, float64-exact integer GEMM) on a row slice of the step."""
-    import numpy as np
-
-    from oracle import oracle as O
-
+def _cpu_model() -> str:
     try:
-        from threadpoolctl import threadpool_info
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
-        threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
-    except Exception:  # pragma: no cover - threadpoolctl is optional
-        threads = os.cpu_count() or 1
-    rng = np.random.default_rng(0)
-    w = rng.integers(-127, 128, (N, K)).astype(np.int8)
-    sw = O.f32_to_bf16(rng.uniform(1e-3, 1e-2, N).astype(np.float32))
+
+def cpu_baseline(budget_s: float) -> dict:
+    """The reference's own CPU path for the step, in torch on this host's cores.
+
+    Quantizer: benchmarks/microbench_quantize.py:75-76 (FP32 row max / 127 floored at
+    1e-20, then round and clamp to +-127). GEMM: tests/test_cuda_ops.py:596-599 (INT32
+    matmul `a.int() @ w.int().T`, then the FP32 epilogue row scale first, channel scale
+    second, rounded to BF16). The full 4096-row step takes minutes on a CPU, so a
+    leading slice of rows is timed (sized to about `budget_s` seconds) and the rate is
+    reported per op, i.e. extrapolated by 4096 / rows to the whole step.
+    """
+    import torch
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    gen = torch.Generator().manual_seed(20261011)
+    w = torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8)
+    sw = (torch.rand(N, generator=gen) * 9e-3 + 1e-3).to(torch.bfloat16)
+    cols = torch.randperm(K, generator=gen)[: max(1, K // 1000)]
 
     def run(rows):
-        x = rng.standard_normal((rows, K)).astype(np.float32)
-        x[:, :5] *= 50
-        x_bits = O.f32_to_bf16(x)
+        x = torch.randn(rows, K, generator=gen)
+        x[:, cols] *= 50
+        x = x.to(torch.bfloat16)
         t0 = time.perf_counter()
-        codes, sa = O.quantize_rows(x_bits)
-        O.fused_channel_mm(codes, w, sa, sw)
-        return time.perf_counter() - t0
+        scale = (x.float().abs().amax(-1) / 127).clamp_min(1e-20)
+        codes = (x.float() / scale[:, None]).round().clamp(-127, 127).to(torch.int8)
+        integer = codes.int() @ w.int().T
+        out = (integer.float() * scale[:, None] * sw.float()[None, :]).to(torch.bfloat16)
+        elapsed = time.perf_counter() - t0
+        assert out.shape == (rows, N)
+        return elapsed
 
-    rows = 64
+    rows = 32
     elapsed = run(rows)
-    rows = int(min(M, max(64, rows * budget_s / max(elapsed, 1e-3))))
+    rows = int(min(M, max(32, rows * budget_s / max(elapsed, 1e-3))))
     elapsed = run(rows)
     tops = 2 * rows * N * K / elapsed / 1e12
     return {
-        "value": round(tops, 4),
+        "value": round(tops, 5),
         "unit": "TOPS",
-        "cores": int(threads),
+        "cores": cores,
         "kind": "port",
-        "sample": f"oracle quantize_rows + fused_channel_mm on {rows} of {M} rows "
-                  f"(K={K}, N={N}), {elapsed:.2f} s; CPU {platform.processor() or platform.machine()}",
+        "path": "the reference's torch CPU math, restated here",
+        "sample": f"reference torch CPU math (benchmarks/microbench_quantize.py:75-76 quantizer, "
+                  f"tests/test_cuda_ops.py:596-599 INT32 matmul + FP32 epilogue) on the first "
+                  f"{rows} of {M} rows (K={K}, N={N}) in {elapsed:.2f} s, extrapolated "
+                  f"x{M / rows:.2f} to the full step ({M / rows * elapsed:.1f} s)",
+        "cpu_model": _cpu_model(),
+        "torch": torch.__version__,
+        "threads": torch.get_num_threads(),
     }
 
 

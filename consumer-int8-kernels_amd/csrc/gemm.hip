@@ -1235,23 +1235,26 @@ using WLds256 = WLdsConfig<256, 8, false>;            // 4 waves, 64x256 per wav
 // tile width, so the cost of a width is rounds x width. 224 suits N = 17408 at M = 4096
 // (1,248 tiles, 4.9 rounds on 256 CUs, where 256-wide tiles need 4.25 rounds, i.e. 5);
 // 256 suits N = 5120 at M = 16384 (5 full rounds against 5.75).
-bool wide_tiles_pay(int m, int n) {
-  int device = 0, cus = 0;
-  if (hipGetDevice(&device) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
-      cus <= 0)
-    return false;
+bool wide_tiles_pay(int m, int n, int cus) {
+  if (cus <= 0) return false;
   const int64_t tiles_m = (m + 255) / 256;
   const int64_t rounds224 = (tiles_m * ((n + 223) / 224) + cus - 1) / cus;
   const int64_t rounds256 = (tiles_m * ((n + 255) / 256) + cus - 1) / cus;
   return rounds256 * 256 < rounds224 * 224;
 }
 
+// Largest M the small-M kernel (gemm_small.hip) takes under schedule 0.
+constexpr int kSmallMaxM = 256;
+
 template <WeightCode kCode, bool kWorkspace>
 hipError_t dispatch(const int8_t* a, const void* w, const float* sa, const void* sw, void* out,
                     int32_t* ws, int m, int n, int k, int schedule, hipStream_t stream) {
+  const int cus = device_cu_count();
+  if (schedule == 0 && m <= kSmallMaxM)
+    return launch_small_m_gemm(a, w, kCode, sa, sw, out, ws, m, n, k, cus > 0 ? cus : 256,
+                               stream);
   int choice = schedule;
-  if (choice == 0) choice = m <= 32 ? 5 : (m < 1024 ? 1 : (wide_tiles_pay(m, n) ? 3 : 4));
+  if (choice == 0) choice = m < 1024 ? 1 : (wide_tiles_pay(m, n, cus) ? 3 : 4);
   switch (choice) {
     case 5:
       return run<Small, kCode, kWorkspace>(a, w, sa, sw, out, ws, m, n, k, stream);
@@ -1397,6 +1400,20 @@ hipError_t run_grouped(const int8_t* a, const int8_t* w, const float* sa, const 
 }
 
 }  // namespace
+
+int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];  // 0 until first queried
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return 0;
+  int cus = cached[device].load(std::memory_order_relaxed);
+  if (cus > 0) return cus;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      cus <= 0)
+    return 0;
+  cached[device].store(cus, std::memory_order_relaxed);
+  return cus;
+}
 
 hipError_t launch_channel_gemm(const int8_t* a, const void* w, WeightCode code,
                                const float* sa, const void* sw, void* out,

@@ -510,10 +510,8 @@ hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale
   // 26 - 27 us for the ring).
   using P = ResidentConfig<16, 5, 4>;
   constexpr int kStaticLds = P::kS * 64 * 16;  // partial sums
-  int device = 0, cus = 0;
-  if (lds + kStaticLds <= 160 * 1024 && hipGetDevice(&device) == hipSuccess &&
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess &&
-      cus > 0) {
+  const int cus = device_cu_count();
+  if (lds + kStaticLds <= 160 * 1024 && cus > 0) {
     auto kernel = channel_gemv_persistent_kernel<P>;
     static std::atomic<bool> configured{false};
     if (const hipError_t e = raise_lds_limit_once(kernel, 160 * 1024 - kStaticLds, configured);

@@ -21,6 +21,15 @@ hipError_t launch_channel_gemm(const int8_t* a, const void* w, WeightCode code,
                                int32_t* workspace, int m, int n, int k, int schedule,
                                hipStream_t stream);
 
+// Small-M variant of launch_channel_gemm (gemm_small.hip): small output tiles, K split
+// over the workgroup's waves; identical bits. `cus` is the device's CU count.
+hipError_t launch_small_m_gemm(const int8_t* a, const void* w, WeightCode code, const float* sa,
+                               const void* sw, void* out, int32_t* workspace, int m, int n,
+                               int k, int cus, hipStream_t stream);
+
+// The current device's CU count, queried once per device and cached (0 if unknown).
+int device_cu_count();
+
 // out = bf16(sum_g (float(A_g W_g^T) * sa[g]) * sw), A [groups, m, k], W [groups, n, k],
 // sa [groups, m]; FP32 sum over ascending g.
 hipError_t launch_grouped_summed_gemm(const int8_t* a, const int8_t* w, const float* sa,
