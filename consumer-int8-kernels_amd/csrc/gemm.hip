@@ -1255,6 +1255,13 @@ hipError_t dispatch(const int8_t* a, const void* w, const float* sa, const void*
                                stream);
   int choice = schedule;
   if (choice == 0) choice = m < 1024 ? 1 : (wide_tiles_pay(m, n, cus) ? 3 : 4);
+  // Signed weights without the INT32 copy: the two-waves-per-SIMD kernel (gemm_pp.hip)
+  // in place of the 224-wide one (its epilogue reads the channel scales 8 bytes at a
+  // time).
+  if constexpr (kCode == WeightCode::kSigned && !kWorkspace) {
+    if (schedule == 0 && choice == 4 && n % 4 == 0 && reinterpret_cast<uintptr_t>(sw) % 8 == 0)
+      return launch_pp_gemm(a, static_cast<const int8_t*>(w), sa, sw, out, m, n, k, stream);
+  }
   switch (choice) {
     case 5:
       return run<Small, kCode, kWorkspace>(a, w, sa, sw, out, ws, m, n, k, stream);

@@ -1,0 +1,317 @@
+// Large-M INT8 GEMM for gfx950 with two waves per SIMD in alternating roles.
+//
+//   out[m, n] = bf16_rn( fl( fl( float_rn(acc[m, n]) * sa[m] ) * float(sw[n]) ) )
+//   acc[m, n] = sum_k a[m, k] * w[n, k]            (exact INT32)
+//
+// the arithmetic of csrc/fused_mm.cu:24-38 (and of gemm.hip, bit for bit).
+//
+// Tile 256 (m) x 224 (n) per workgroup of eight waves. Wave w owns rows 64 * (w % 4)
+// and columns 112 * (w / 4) of the tile, as 4 x 7 blocks of v_mfma_i32_16x16x64_i8
+// accumulators (112 registers). Waves w and w + 4 share SIMD w % 4. The waves of group
+// g = w / 4 alternate between a memory phase (read the stage's 22 MFMA fragments from
+// LDS and issue this wave's copies of a later stage) and a compute phase (56 MFMAs from
+// registers), and the two groups are offset by one phase, so each SIMD always has one
+// wave issuing MFMAs while the other waits on memory. Phases end at workgroup barriers:
+//
+//   phase:     0        1        2        3        4      ...
+//   group 0:   M0       C0       M1       C1       M2
+//   group 1:   -        M0       C0       M1       C1
+//
+// Measured on MI355X (per-wave clock stamps), one wave of each SIMD issuing 56 MFMAs
+// while the other reads its fragments keeps the MFMA pipes about 96% busy when the
+// operands are already in LDS; where a single wave per SIMD does both, the lock-step
+// barriers of its K loop idle the pipes about a quarter of the time.
+//
+// Operands go through LDS rings of 128-byte K stages filled by buffer_load ... lds
+// (8 rows x 128 bytes per copy; rows past M or N and bytes past K come back as zeros
+// from the buffer range check). Copies are issued between the fragment reads of the
+// memory phases: the vector-memory unit takes about 16 cycles per 1 KiB copy per CU and
+// a wave stalls when it issues into a full queue, which in a compute phase would stall
+// the MFMAs (measured: about 40 cycles per copy there). Group 0 copies A, group 1 W:
+//   A: two 32 KB slots. A(t + 1) is copied in phase 2t into the slot of A(t - 1), which
+//      both groups read in phases 2t - 2 and 2t - 1; group 0 waits for it at the end of
+//      phase 2t + 1.
+//   W: three 28 KB slots. W(t + 2) is copied in phase 2t + 1 into the slot of W(t - 1),
+//      read in phases 2t - 2 and 2t - 1; group 1 waits for W(t + 1) at the end of phase
+//      2t + 1.
+// A W wave has 7 copies per stage against an A wave's 8; its eighth reads nothing into a
+// junk KiB, which keeps the copy sequence identical and branch-free.
+//
+// MFMA lane layouts are those of gemm.hip: the MFMA computes D[n][m] = W . A^T, within a
+// 128-byte stage lane group g (lane / 16) reads logical chunk 2g + h in K-step h, and
+// LDS rows hold their 16-byte chunks XOR-swizzled by row % 8.
+#include "ci8_device.h"
+#include "launch.h"
+
+namespace ci8 {
+namespace {
+
+constexpr int kXcds = 8;
+
+struct PPConfig {
+  static constexpr int BM = 256, BN = 224, BK = 128;
+  static constexpr int kWaves = 8, kThreads = 512;
+  static constexpr int WM = 4;                        // waves along m (per group)
+  static constexpr int TM = BM / WM / 16;             // 4 m blocks per wave
+  static constexpr int TN = BN / 2 / 16;              // 7 n blocks per wave
+  static constexpr int kABlocks = BM * BK / 1024;     // 32 copies of A per stage
+  static constexpr int kWBlocks = BN * BK / 1024;     // 28 copies of W per stage
+  static constexpr int kCopies = kABlocks / WM;       // per wave per stage (8)
+  static constexpr int kAStage = BM * BK;             // 32 KB
+  static constexpr int kWStage = BN * BK;             // 28 KB
+  static constexpr int kWBase = 2 * kAStage;          // A ring: 2 slots, W ring: 3 slots
+  static constexpr int kJunk = kWBase + 3 * kWStage;  // 148 KB
+  static constexpr int kRingBytes = kJunk + 1024;
+  // Epilogue staging (reuses the ring): each wave's 64 x 112 BF16 outputs at a row
+  // stride of 240 bytes (60 dwords: 16 rows written by one ds_write_b64 start in
+  // distinct banks).
+  static constexpr int kEpiRowBytes = (BN / 2) * 2 + 16;
+  static constexpr int kEpiWaveBytes = (BM / WM) * kEpiRowBytes;
+  static constexpr int kLdsBytes =
+      kRingBytes > kWaves * kEpiWaveBytes ? kRingBytes : kWaves * kEpiWaveBytes;
+  static constexpr int GROUP_M = 8;
+  static_assert(kCopies * WM == kABlocks && (kCopies - 1) * WM == kWBlocks, "copies");
+  static_assert(3 * (kCopies - 1) < 2 * (TM + TN), "copies fit between the fragment reads");
+  static_assert(kLdsBytes <= 160 * 1024, "LDS");
+};
+
+__device__ __forceinline__ i32x4 lds16(const char __attribute__((address_space(3)))* p) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) i32x4*>(p);
+}
+__device__ __forceinline__ void barrier_fenced() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <bool kExactK>
+__global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
+    const int8_t* __restrict__ a, const int8_t* __restrict__ w, const float* __restrict__ sa,
+    const uint16_t* __restrict__ sw, uint16_t* __restrict__ out, int m, int n, int k,
+    bool out16) {
+  using C = PPConfig;
+  extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
+  auto* lds = (char __attribute__((address_space(3)))*)(lds_raw);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave % C::WM, group = wave / C::WM;
+  const bool copies_a = group == 0;
+
+  // Workgroup -> tile: undo the round-robin dealing over the 8 XCDs, then a grouped
+  // raster of GROUP_M m tiles, so tiles that run together on one XCD share panels.
+  const int tiles_n = (n + C::BN - 1) / C::BN;
+  const int tiles_m = (m + C::BM - 1) / C::BM;
+  const int blocks = tiles_n * tiles_m;
+  int logical = blockIdx.x;
+  {
+    const int per = blocks / kXcds, extra = blocks % kXcds;
+    const int xcd = logical % kXcds, idx = logical / kXcds;
+    logical = (xcd < extra ? xcd * (per + 1) : extra * (per + 1) + (xcd - extra) * per) + idx;
+  }
+  const int group_span = C::GROUP_M * tiles_n;
+  const int first_m = (logical / group_span) * C::GROUP_M;
+  const int group_rows = min(tiles_m - first_m, C::GROUP_M);
+  const int tile_m = first_m + (logical % group_span) % group_rows;
+  const int tile_n = (logical % group_span) / group_rows;
+  const int m0 = tile_m * C::BM, n0 = tile_n * C::BN;
+
+  const auto a_rsrc = make_rsrc(a, uint32_t(m) * uint32_t(k));
+  const auto w_rsrc = make_rsrc(w, uint32_t(n) * uint32_t(k));
+  const auto c_rsrc = copies_a ? a_rsrc : w_rsrc;
+  const int ns = (k + C::BK - 1) / C::BK;
+
+  // Copy i of a wave brings block b = 4i + wave % 4 of its operand's stage (8 rows x 128
+  // bytes): lane -> row 8b + lane / 8, LDS chunk slot lane % 8 holding logical chunk
+  // slot ^ (row % 8). The stage's K offset goes in soffset.
+  const int sub = wave % C::WM;
+  const int c_row = lane >> 3;
+  const int c_chunk = (lane & 7) ^ c_row;
+  uint32_t c_off[C::kCopies];
+#pragma unroll
+  for (int i = 0; i < C::kCopies; ++i) {
+    const int row = (copies_a ? m0 : n0) + (i * C::WM + sub) * 8 + c_row;
+    const bool valid = (copies_a || i < C::kCopies - 1) && row < (copies_a ? m : n);
+    c_off[i] = valid ? uint32_t(row) * uint32_t(k) + uint32_t(c_chunk * 16) : kOutOfRange;
+  }
+  // LDS destination of copy i into ring slot `slot`: c_dst0 + slot * c_stride + 4096 i
+  // (integer arithmetic on wave-uniform values), except a W wave's eighth (junk KiB).
+  const int c_dst0 = (copies_a ? 0 : C::kWBase) + sub * 1024;
+  const int c_stride = copies_a ? C::kAStage : C::kWStage;
+  // A copy of stage t < 0 reads nothing (out of range), into the free slot.
+  auto copy = [&] __device__(int dst, int t, int i) __attribute__((always_inline)) {
+    int to = dst + i * C::WM * 1024;
+    if (i == C::kCopies - 1) to = copies_a ? to : C::kJunk;
+    const int k0 = t < 0 ? 0 : t * C::BK;
+    uint32_t off = t < 0 ? kOutOfRange : c_off[i];
+    if (!kExactK && off != kOutOfRange && k0 + c_chunk * 16 >= k) off = kOutOfRange;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c_rsrc, reinterpret_cast<lds_void*>(lds + to), 16,
+                                             off, k0, 0, 0);
+  };
+
+  // Fragments: row (lane % 16) of each 16-row block at logical chunk 2 * (lane / 16) + h.
+  const int f_row = lane & 15, f_group = lane >> 4;
+  int a_base[2], w_base[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int swz = (((2 * f_group + h) ^ (f_row & 7)) * 16);
+    a_base[h] = (wm * 64 + f_row) * C::BK + swz;
+    w_base[h] = C::kWBase + (group * 112 + f_row) * C::BK + swz;
+  }
+  i32x4 af[2][C::TM], wf[2][C::TN];
+  // Memory phase: the 22 fragments of the stage in A slot a_slot and W slot w_slot, with
+  // this wave's 8 copies of stage copy_t into `dst` after fragment reads 0, 3, ..., 21.
+  auto memory = [&] __device__(int a_slot, int w_slot, int dst, int copy_t)
+                    __attribute__((always_inline)) {
+    const auto* as = lds + a_slot * C::kAStage;
+    const auto* ws = lds + w_slot * C::kWStage;
+#pragma unroll
+    for (int q = 0; q < 2 * (C::TM + C::TN); ++q) {
+      const int h = q / (C::TM + C::TN), r = q % (C::TM + C::TN);
+      if (r < C::TM)
+        af[h][r] = lds16(as + a_base[h] + r * 16 * C::BK);
+      else
+        wf[h][r - C::TM] = lds16(ws + w_base[h] + (r - C::TM) * 16 * C::BK);
+      if (q % 3 == 0) copy(dst, copy_t, q / 3);
+    }
+    __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+  };
+
+  i32x4 acc[C::TM][C::TN];
+#pragma unroll
+  for (int j = 0; j < C::TM; ++j)
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i) acc[j][i] = i32x4{0, 0, 0, 0};
+  auto compute = [&] __device__() __attribute__((always_inline)) {
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < C::TN; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TM; ++j)
+          acc[j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[h][i], af[h][j], acc[j][i], 0, 0, 0);
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  // Prologue: A(0) (group 0), W(0) and W(1) (group 1) in place for everyone.
+#pragma unroll
+  for (int i = 0; i < C::kCopies; ++i) copy(c_dst0, 0, i);
+  if (!copies_a && 1 < ns) {
+#pragma unroll
+    for (int i = 0; i < C::kCopies; ++i) copy(c_dst0 + c_stride, 1, i);
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  barrier_fenced();
+
+  // Stage t: group 0 copies A(t + 1) (into A slot (t + 1) % 2), group 1 W(t + 2) (into W
+  // slot (t + 2) % 3); copies past the last stage read nothing into that free slot.
+  int w_slot = 0;   // t % 3
+  int cw_slot = 2;  // (t + 2) % 3
+  const int lead = copies_a ? 1 : 2;
+  if (group == 1) barrier_fenced();  // phase 0 is group 0's first memory phase
+  for (int t = 0; t < ns; ++t) {
+    const int copy_t = t + lead < ns ? t + lead : -1;
+    const int dst = c_dst0 + (copies_a ? (t + 1) & 1 : cw_slot) * c_stride;
+    memory(t & 1, w_slot, dst, copy_t);
+    // Group 1: W(t + 1) landed (W(t + 2), just issued, may be in flight).
+    if (group == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(C::kCopies));
+    barrier_fenced();
+    compute();
+    // Group 0: A(t + 1), issued in the memory phase, landed.
+    if (group == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    barrier_fenced();
+    w_slot = w_slot == 2 ? 0 : w_slot + 1;
+    cw_slot = cw_slot == 2 ? 0 : cw_slot + 1;
+  }
+  if (group == 0) barrier_fenced();  // phase 2 ns: group 1's last compute phase
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // copies past the end, into free slots
+  barrier_fenced();                          // every wave's copies landed: ring is free
+
+  // Epilogue through LDS: the wave's 64 x 112 BF16 results go to its own region in the
+  // MFMA layout and come back as 16-byte row chunks, so each store instruction writes
+  // whole 224-byte row pieces (14 lanes per row).
+  const int row0 = m0 + wm * 64;
+  const int col0 = n0 + group * 112;
+  float rs[C::TM];
+#pragma unroll
+  for (int j = 0; j < C::TM; ++j) {
+    const int row = row0 + j * 16 + f_row;
+    rs[j] = row < m ? sa[row] : 0.f;
+  }
+  u32x2 s2[C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TN; ++i) {
+    const int col = col0 + i * 16 + f_group * 4;
+    s2[i] = col < n ? *reinterpret_cast<const u32x2*>(sw + col) : u32x2{0, 0};
+  }
+  auto* region = lds + wave * C::kEpiWaveBytes;
+#pragma unroll
+  for (int j = 0; j < C::TM; ++j) {
+    auto* rbase = region + (j * 16 + f_row) * C::kEpiRowBytes + f_group * 8;
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i) {
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t bits = (s2[i][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+        v[e] = (float(acc[j][i][e]) * rs[j]) * bf16_to_f32(bits);
+      }
+      *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(rbase + i * 32) =
+          u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    }
+  }
+  // One wave's LDS operations complete in order; the wait only orders the reads after
+  // every lane's writes for the compiler.
+  __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+  __builtin_amdgcn_wave_barrier();
+  constexpr int kChunks = 112 / 8;  // 16-byte chunks per output row piece
+  const bool full = out16 && row0 + 64 <= m && col0 + 112 <= n && (n % 8) == 0;
+#pragma unroll
+  for (int it = 0; it < kChunks; ++it) {
+    const int q = it * 64 + lane;
+    const int row = q / kChunks, chunk = q % kChunks;
+    const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+        region + row * C::kEpiRowBytes + chunk * 16);
+    const int grow = row0 + row, gcol = col0 + chunk * 8;
+    uint16_t* dst = out + int64_t(grow) * n + gcol;
+    if (full) {
+      *reinterpret_cast<u32x4*>(dst) = v;
+    } else if (grow < m) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (gcol + e < n) dst[e] = uint16_t(v[e >> 1] >> (16 * (e & 1)));
+    }
+  }
+}
+
+}  // namespace
+
+// Requires a and w 16-byte aligned, sw 8-byte aligned and n % 4 == 0 (the fused op's
+// contract); out needs 2-byte alignment (16-byte aligned rows take 16-byte stores).
+hipError_t launch_pp_gemm(const int8_t* a, const int8_t* w, const float* sa, const void* sw,
+                          void* out, int m, int n, int k, hipStream_t stream) {
+  using C = PPConfig;
+  const int blocks = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
+  const bool out16 = (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  if (k % C::BK == 0) {
+    auto kernel = pp_gemm_kernel<true>;
+    static std::atomic<bool> configured{false};
+    if (const hipError_t e = raise_lds_limit_once(kernel, C::kLdsBytes, configured); e != hipSuccess)
+      return e;
+    kernel<<<blocks, C::kThreads, C::kLdsBytes, stream>>>(
+        a, w, sa, static_cast<const uint16_t*>(sw), static_cast<uint16_t*>(out), m, n, k, out16);
+  } else {
+    auto kernel = pp_gemm_kernel<false>;
+    static std::atomic<bool> configured{false};
+    if (const hipError_t e = raise_lds_limit_once(kernel, C::kLdsBytes, configured); e != hipSuccess)
+      return e;
+    kernel<<<blocks, C::kThreads, C::kLdsBytes, stream>>>(
+        a, w, sa, static_cast<const uint16_t*>(sw), static_cast<uint16_t*>(out), m, n, k, out16);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace ci8
