@@ -1,16 +1,20 @@
 """Channel-UINT8 checkpoint encoding and loading for the INT8 linear layers.
 
 `encode` converts an unquantized Qwen3.8-27B safetensors snapshot into the reference's
-published encoding (src/consumer_int8/checkpoint.py:58-171): the language-model and MTP
-linear weights become biased UINT8 codes plus BF16 `*.weight_scale_inv` channel scales,
-the vision tower's linear weights become signed INT8 plus FP32 `*.weight_scale` group
-scales, and every other tensor passes through. Shard ownership, the tensor inventory,
-the per-tensor error report, the index and the `quantization_config` are those of the
-reference, and the same inputs are refused with the same messages. `device` selects
-where the quantization arithmetic runs: "cuda" encodes on the MI355X with results
-bit-identical to the host's (the codes and scales are IEEE FP32 operations with one
-correct rounding each); the report's error statistics are reductions and may differ in
-their last bits.
+published encoding (the format written by src/consumer_int8/checkpoint.py:58-171): the
+language-model and MTP linear weights become biased UINT8 codes plus BF16
+`*.weight_scale_inv` channel scales, the vision tower's linear weights become signed
+INT8 plus FP32 `*.weight_scale` group scales, and every other tensor passes through.
+The files, tensor names, shard ownership, report fields, index and `quantization_config`
+are that format, and the same inputs are refused with the same messages. The encoder
+itself is organised differently: it plans and checks the whole snapshot before writing
+anything (a snapshot refused for its layout leaves the destination empty; only
+non-finite weights are found while encoding), then encodes shard by shard.
+
+`device` selects where the quantization arithmetic runs: "cuda" encodes on the MI355X
+with results bit-identical to the host's (the codes and scales are IEEE FP32 operations
+with one correct rounding each); the report's error statistics are reductions and may
+differ in their last bits.
 
 `load_channel_linear` is the loading side, for the ops of this package: it reads one
 channel-UINT8 layer back onto a device, debiased to signed INT8 for fused_channel_mm
@@ -62,8 +66,11 @@ _VISION_NAME = re.compile(
     r"|merger\.linear_fc1|merger\.linear_fc2)\.weight"
 )
 
-_COPIED_SUFFIXES = {".json", ".txt", ".jinja"}
-_NOT_COPIED = {"config.json", "model.safetensors.index.json", "crc32.txt"}
+# Files of the snapshot published next to the shards: small text sidecars (tokenizer,
+# chat template, generation config, ...) and the licence, but not the files the encoder
+# rewrites itself or the source's checksum list.
+_SIDECAR_SUFFIXES = (".json", ".txt", ".jinja")
+_REWRITTEN = ("config.json", "model.safetensors.index.json", "crc32.txt")
 
 
 def encoding_for(name: str) -> str:
@@ -82,114 +89,151 @@ def scale_name_for(name: str, encoding: str) -> str:
     return stem + (".weight_scale_inv" if encoding == "channel_uint8" else ".weight_scale")
 
 
-def _sha256(path: Path) -> str:
+def _file_sha256(path: Path) -> str:
     digest = hashlib.sha256()
     with path.open("rb") as stream:
-        while block := stream.read(8 << 20):
-            digest.update(block)
+        while chunk := stream.read(1 << 23):
+            digest.update(chunk)
     return digest.hexdigest()
 
 
-def _publish_json(path: Path, value: dict) -> None:
-    """Write through a temporary file and rename, so readers never see half a file."""
-    pending = path.with_name(path.name + ".tmp")
-    pending.write_text(json.dumps(value, indent=2) + "\n")
-    pending.replace(path)
+def _atomic_json(path: Path, value: dict) -> None:
+    """Publish `value` at `path` by writing a sibling and renaming it over the target, so
+    a reader sees either the old file or the whole new one."""
+    staged = path.parent / f"{path.name}.tmp"
+    staged.write_text(json.dumps(value, indent=2) + "\n")
+    staged.replace(path)
 
 
-def _check_source(source: Path, destination: Path) -> tuple[dict, dict]:
-    # src/consumer_int8/checkpoint.py:59-76
+class _Job:
+    """One source tensor: how it is stored and under which extra name its scales go."""
+
+    __slots__ = ("name", "encoding", "scale_name")
+
+    def __init__(self, name: str):
+        self.name = name
+        self.encoding = encoding_for(name)
+        self.scale_name = (None if self.encoding == "passthrough"
+                           else scale_name_for(name, self.encoding))
+
+
+def _plan(source: Path, destination: Path) -> tuple[dict, dict[str, list[_Job]]]:
+    """Everything that can refuse a snapshot without encoding it, done before the first
+    byte is written: the directories, the architecture and geometry of the config (the
+    manifest targets Qwen3.8-27B only), the MTP and vision parts of the index, shard file
+    names, the tensors each shard actually holds, and scale names that would collide with
+    source tensors. The refusals carry the reference's messages
+    (src/consumer_int8/checkpoint.py:59-76, :86-90, :110-111). Returns the config and,
+    per shard in sorted order, the jobs of its tensors in sorted name order."""
     if source.resolve() == destination.resolve():
         raise ValueError("Source and destination must differ")
-    if destination.exists() and any(destination.iterdir()):
+    if destination.exists() and next(destination.iterdir(), None) is not None:
         raise ValueError("Destination must be empty; partial conversions are not models")
     config = json.loads((source / "config.json").read_text())
     if config.get("model_type") != "qwen3_5" or config.get("quantization_config"):
         raise ValueError("Expected an unquantized Qwen3.5 architecture checkpoint")
-    text = config["text_config"]
-    if (text["hidden_size"], text["num_hidden_layers"]) != (5120, 64):
+    geometry = config["text_config"]
+    if geometry["hidden_size"] != 5120 or geometry["num_hidden_layers"] != 64:
         raise ValueError("This encoding manifest targets Qwen3.8-27B geometry")
-    weight_map = json.loads((source / "model.safetensors.index.json").read_text())["weight_map"]
-    if not any(name.startswith("mtp.") for name in weight_map):
-        raise ValueError("The full checkpoint must contain MTP weights")
-    if not any(name.startswith("model.visual.") for name in weight_map):
-        raise ValueError("The full checkpoint must contain vision weights")
-    return config, weight_map
+    owner = json.loads((source / "model.safetensors.index.json").read_text())["weight_map"]
+    for part, prefix in (("MTP", "mtp."), ("vision", "model.visual.")):
+        if not any(name.startswith(prefix) for name in owner):
+            raise ValueError(f"The full checkpoint must contain {part} weights")
+
+    by_shard: dict[str, list[str]] = {}
+    for name, shard in owner.items():
+        by_shard.setdefault(shard, []).append(name)
+    shards: dict[str, list[_Job]] = {}
+    for shard in sorted(by_shard):
+        if Path(shard).name != shard:
+            raise ValueError(f"Invalid shard filename: {shard}")
+        with safe_open(source / shard, framework="pt", device="cpu") as handle:
+            held = set(handle.keys())
+        if held != set(by_shard[shard]):
+            raise ValueError(f"Index and shard disagree: {shard}")
+        jobs = [_Job(name) for name in sorted(held)]
+        for job in jobs:
+            if job.scale_name is not None and job.scale_name in owner:
+                raise ValueError(f"Scale name already exists: {job.scale_name}")
+        shards[shard] = jobs
+    return config, shards
 
 
-def _encode_tensor(name: str, weight: torch.Tensor, device: str, source_names) -> tuple[dict, dict]:
-    """Encoded tensors of one source tensor and its report record (:97-118)."""
-    encoding = encoding_for(name)
-    record = {"shape": list(weight.shape), "encoding": encoding}
-    if encoding == "passthrough":
-        tensors = {name: weight}
+def _quantize(job: _Job, weight: torch.Tensor, device: str):
+    """Codes, scales and the report's error statistics of one quantized tensor (the
+    reference's arithmetic, src/consumer_int8/checkpoint.py:100-118)."""
+    on_device = weight.to(device)
+    if job.encoding == "channel_uint8":
+        codes, scales = quantize_channel(on_device)
+        error = dequantize_channel(codes, scales) - on_device.float()
     else:
-        on_device = weight.to(device)
-        if encoding == "channel_uint8":
-            codes, scales = quantize_channel(on_device)
-            restored = dequantize_channel(codes, scales)
-        else:
-            codes, scales = quantize_group32(on_device)
-            restored = dequantize_group32(codes, scales)
-        scale_name = scale_name_for(name, encoding)
-        if scale_name in source_names:
-            raise ValueError(f"Scale name already exists: {scale_name}")
-        error = restored - on_device.float()
-        record["rmse"] = error.square().mean().sqrt().item()
-        record["max_abs_error"] = error.abs().max().item()
-        tensors = {name: codes.cpu(), scale_name: scales.cpu()}
-    record["stored_dtype"] = str(tensors[name].dtype)
-    return tensors, record
+        codes, scales = quantize_group32(on_device)
+        error = dequantize_group32(codes, scales) - on_device.float()
+    stats = {"rmse": error.square().mean().sqrt().item(),
+             "max_abs_error": error.abs().max().item()}
+    return codes.cpu(), scales.cpu(), stats
 
 
 def encode(source: Path, destination: Path, *, source_revision: str, device: str = "cpu") -> dict:
     """Encode the checkpoint at `source` into the empty directory `destination`; returns
-    the encoding report (also written as encoding_report.json). The config is published
-    last, so an interrupted conversion never looks loadable (:164-166)."""
+    the encoding report (also written as encoding_report.json).
+
+    The snapshot is planned and checked in full first (`_plan`), then encoded one shard
+    at a time: each shard's tensors go to a staged file renamed into place once complete,
+    and the report is republished after every shard, so progress is visible and every
+    published shard is whole. The index, the final report and, last of all, the config
+    (which is what makes a directory loadable) follow the shards."""
     source, destination = Path(source), Path(destination)
-    config, source_map = _check_source(source, destination)
+    config, shards = _plan(source, destination)
     destination.mkdir(parents=True, exist_ok=True)
-    report = {
-        "format_version": 1,
-        "encoder_version": __version__,
-        "source_repo": SOURCE_REPO,
-        "source_revision": source_revision,
-        "status": "encoding",
-        "tensors": {},
-        "shards": {},
-    }
-    weight_map: dict[str, str] = {}
-    total_size = 0
-    for shard in sorted(set(source_map.values())):
-        if Path(shard).name != shard:
-            raise ValueError(f"Invalid shard filename: {shard}")
-        owned = {name for name, owner in source_map.items() if owner == shard}
-        output: dict[str, torch.Tensor] = {}
+
+    records: dict[str, dict] = {}
+    shard_records: dict[str, dict] = {}
+    stored_in: dict[str, str] = {}
+    stored_bytes = 0
+
+    def report(status: str) -> dict:
+        return {"format_version": 1, "encoder_version": __version__,
+                "source_repo": SOURCE_REPO, "source_revision": source_revision,
+                "status": status, "tensors": records, "shards": shard_records}
+
+    for shard, jobs in shards.items():
+        tensors: dict[str, torch.Tensor] = {}
         with safe_open(source / shard, framework="pt", device="cpu") as handle:
-            if set(handle.keys()) != owned:
-                raise ValueError(f"Index and shard disagree: {shard}")
-            for name in sorted(owned):
-                tensors, record = _encode_tensor(name, handle.get_tensor(name), device, source_map)
-                output.update(tensors)
-                report["tensors"][name] = record
-        pending = destination / (shard + ".tmp")
-        save_file(output, pending, metadata={"format": "pt"})
-        pending.replace(destination / shard)
-        for name, tensor in output.items():
-            weight_map[name] = shard
-            total_size += tensor.numel() * tensor.element_size()
-        report["shards"][shard] = {"sha256": _sha256(destination / shard),
-                                   "tensor_count": len(output)}
-        del output
-        _publish_json(destination / "encoding_report.json", report)
+            for job in jobs:
+                weight = handle.get_tensor(job.name)
+                record = {"shape": list(weight.shape), "encoding": job.encoding}
+                if job.scale_name is None:
+                    tensors[job.name] = weight
+                else:
+                    codes, scales, stats = _quantize(job, weight, device)
+                    tensors[job.name], tensors[job.scale_name] = codes, scales
+                    record.update(stats)
+                record["stored_dtype"] = str(tensors[job.name].dtype)
+                records[job.name] = record
+        staged = destination / f"{shard}.tmp"
+        save_file(tensors, staged, metadata={"format": "pt"})
+        staged.replace(destination / shard)
+        stored_in.update(dict.fromkeys(tensors, shard))
+        stored_bytes += sum(t.numel() * t.element_size() for t in tensors.values())
+        shard_records[shard] = {"sha256": _file_sha256(destination / shard),
+                                "tensor_count": len(tensors)}
+        tensors.clear()
+        _atomic_json(destination / "encoding_report.json", report("encoding"))
         print(f"Encoded {shard}", flush=True)
-    if set(report["tensors"]) != set(source_map):
+
+    planned = {job.name for jobs in shards.values() for job in jobs}
+    if set(records) != planned:
         raise RuntimeError("Conversion did not preserve the source tensor inventory")
+
     for path in source.iterdir():
-        if path.is_file() and path.suffix in _COPIED_SUFFIXES and path.name not in _NOT_COPIED:
+        sidecar = (path.is_file() and path.suffix in _SIDECAR_SUFFIXES
+                   and path.name not in _REWRITTEN)
+        if sidecar or path.name == "LICENSE":
             shutil.copy2(path, destination / path.name)
-        elif path.name == "LICENSE":
-            shutil.copy2(path, destination / path.name)
+
+    quantized = {name.removesuffix(".weight"): rec["encoding"]
+                 for name, rec in records.items() if rec["encoding"] != "passthrough"}
     config["quantization_config"] = {
         "quant_method": "qwen_int8",
         "format_version": 1,
@@ -197,19 +241,15 @@ def encode(source: Path, destination: Path, *, source_revision: str, device: str
         "vision_weight_strategy": "group32_int8",
         "source_repo": SOURCE_REPO,
         "source_revision": source_revision,
-        "quantized_modules": {
-            name.removesuffix(".weight"): record["encoding"]
-            for name, record in report["tensors"].items()
-            if record["encoding"] != "passthrough"
-        },
+        "quantized_modules": quantized,
     }
-    _publish_json(destination / "model.safetensors.index.json",
-                  {"metadata": {"total_size": total_size}, "weight_map": weight_map})
-    report["status"] = "encoded_unvalidated"
-    report["total_tensor_bytes"] = total_size
-    _publish_json(destination / "encoding_report.json", report)
-    _publish_json(destination / "config.json", config)
-    return report
+    _atomic_json(destination / "model.safetensors.index.json",
+                 {"metadata": {"total_size": stored_bytes}, "weight_map": stored_in})
+    final = report("encoded_unvalidated")
+    final["total_tensor_bytes"] = stored_bytes
+    _atomic_json(destination / "encoding_report.json", final)
+    _atomic_json(destination / "config.json", config)
+    return final
 
 
 def load_channel_linear(checkpoint: Path, module: str, device="cuda", signed: bool = True):

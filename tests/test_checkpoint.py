@@ -286,6 +286,8 @@ def test_encode_refusals(tmp_path):
     (bad / "model.safetensors.index.json").write_text(json.dumps(index))
     with pytest.raises(ValueError, match="Index and shard disagree"):
         encode(bad, tmp_path / "o5", source_revision="r")
+    # layout refusals come before anything is written
+    assert not (tmp_path / "o5").exists()
     # a shard name with a directory part
     sub = variant("sub")
     index = json.loads((sub / "model.safetensors.index.json").read_text())
@@ -299,6 +301,7 @@ def test_encode_refusals(tmp_path):
     clash_layout["model-00002-of-00002.safetensors"]["mtp.fc.weight_scale_inv"] = (48,)
     with pytest.raises(ValueError, match="Scale name already exists: mtp.fc.weight_scale_inv"):
         encode(variant("clash", layout=clash_layout), tmp_path / "o7", source_revision="r")
+    assert not (tmp_path / "o7").exists()
     # non-finite weights are refused by the encoders
     nan = variant("nan")
     shard = "model-00002-of-00002.safetensors"
