@@ -38,6 +38,8 @@ SIGNATURES = {
     "ci8_quantize_block32": ([_p, _p, _p, _i64, _i64, _p], ctypes.c_int),
     "ci8_q8_block_mm": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p], ctypes.c_int),
     "ci8_q8_block_int8": ([_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p], ctypes.c_int),
+    "ci8_gguf_q8_packed_mm": ([_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p],
+                              ctypes.c_int),
 }
 
 _lib = None

@@ -250,4 +250,39 @@ int ci8_q8_block_int8(const void* x, int8_t* a, float* sa, const int8_t* w, cons
   return launched(ci8::launch_q8_block_mm(a, sa, w, sw, y, int(m), int(n), int(k), s));
 }
 
+// csrc/gguf_bindings.cpp:135-171, the same checks in the same order.
+int ci8_gguf_q8_packed_mm(const void* x, const int8_t* codes, const void* scales, void* out,
+                          int64_t m, int64_t n, int64_t k, int64_t groups,
+                          int64_t x_row_stride, int64_t x_group_stride, void* stream) {
+  if (!(m >= 0 && n >= 0 && groups >= 0 && k > 0 && k % 64 == 0 && x_row_stride > 0 &&
+        x_group_stride > 0))
+    return fail(CI8_ERR_GEOMETRY, "Invalid packed Q8 shape/strides; K must be a multiple of 64");
+  if (!(m <= 65535LL * 32 && groups <= 65535 && k <= 2147483584LL && n <= 2147483584LL))
+    return fail(CI8_ERR_TOO_LARGE, "Packed Q8 grid too large");
+  if (x_row_stride % 8 || x_group_stride % 8 || !aligned(x, 16) || !aligned(codes, 16) ||
+      !aligned(scales, 4))
+    return fail(CI8_ERR_ALIGNMENT, "Packed Q8 copy alignment violation");
+  if (m == 0 || n == 0 || groups == 0) {
+    g_last_error.clear();
+    return CI8_OK;
+  }
+  // Byte extents in 128-bit arithmetic: no device buffer reaches 2^62 bytes, so larger
+  // extents (which would also overflow the kernels' 64-bit offsets) are rejected.
+  using u128 = unsigned __int128;
+  const u128 out_extent = u128(m) * u128(groups) * u128(n) * 2;
+  const u128 x_extent =
+      (u128(m - 1) * u128(x_row_stride) + u128(groups - 1) * u128(x_group_stride) + u128(k)) * 2;
+  const u128 codes_extent = u128(groups) * u128(n) * u128(k);
+  constexpr u128 kMaxExtent = u128(1) << 62;
+  if (out_extent > kMaxExtent || x_extent > kMaxExtent || codes_extent > kMaxExtent)
+    return fail(CI8_ERR_TOO_LARGE, "Packed Q8 grid too large");
+  const auto out_bytes = int64_t(out_extent), x_bytes = int64_t(x_extent);
+  if (overlap(out, out_bytes, x, x_bytes) || overlap(out, out_bytes, codes, groups * n * k) ||
+      overlap(out, out_bytes, scales, groups * n * (k / 32) * 2))
+    return fail(CI8_ERR_OVERLAP, "Packed Q8 output must not alias inputs");
+  return launched(ci8::launch_gguf_q8_packed_mm(x, codes, scales, out, int(m), int(n), int(k),
+                                                int(groups), x_row_stride, x_group_stride,
+                                                as_stream(stream)));
+}
+
 }  // extern "C"

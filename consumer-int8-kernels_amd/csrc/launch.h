@@ -63,6 +63,13 @@ hipError_t launch_q8_block_mm(const int8_t* a, const float* sa, const int8_t* w,
                               const void* sw, void* y, int m, int n, int k,
                               hipStream_t stream);
 
+// Grouped W8A16 on GGUF Q8_0 codes: x BF16 [m, groups, k] (row stride xs, group stride
+// xg elements), codes INT8 [groups, n, k], scales FP16 [groups, n, k/32] -> out BF16
+// [m, groups, n]. Requires k % 64 == 0, x and codes 16-byte aligned, xs, xg % 8 == 0.
+hipError_t launch_gguf_q8_packed_mm(const void* x, const int8_t* codes, const void* scales,
+                                    void* out, int m, int n, int k, int groups, int64_t xs,
+                                    int64_t xg, hipStream_t stream);
+
 hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale, void* out,
                                int m, int n, int k, hipStream_t stream);
 

@@ -238,10 +238,39 @@ void unpack_allspark(Tensor packed, Tensor packed_scales, Tensor weight, Tensor 
                                      n, k, stream_for(device)));
 }
 
+// csrc/gguf_bindings.cpp:135-171: x may be strided over rows and groups (K contiguous);
+// the C ABI checks strides, sizes, alignment and aliasing.
+void gguf_q8_packed_mm(Tensor x, Tensor codes, Tensor scales, Tensor out) {
+  const int device = x.get_device_index();
+  STD_TORCH_CHECK(x.is_cuda() && codes.is_cuda() && scales.is_cuda() && out.is_cuda() &&
+                      codes.get_device_index() == device &&
+                      scales.get_device_index() == device && out.get_device_index() == device,
+                  "Packed Q8 tensors must share a CUDA device");
+  STD_TORCH_CHECK(x.scalar_type() == ScalarType::BFloat16 &&
+                      codes.scalar_type() == ScalarType::Char &&
+                      scales.scalar_type() == ScalarType::Half &&
+                      out.scalar_type() == ScalarType::BFloat16,
+                  "Packed Q8 requires BF16 input/output, INT8 codes and original FP16 scales");
+  STD_TORCH_CHECK(x.dim() == 3 && codes.dim() == 3 && scales.dim() == 3 && out.dim() == 3,
+                  "Expected x[M,G,K], q[G,N,K], scales[G,N,K/32], out[M,G,N]");
+  const int64_t m = x.size(0), groups = x.size(1), k = x.size(2), n = codes.size(1);
+  STD_TORCH_CHECK(codes.is_contiguous() && scales.is_contiguous() && out.is_contiguous() &&
+                      x.stride(2) == 1 && x.stride(0) > 0 && x.stride(1) > 0 && k > 0 &&
+                      k % 64 == 0 && codes.size(0) == groups && codes.size(2) == k &&
+                      scales.size(0) == groups && scales.size(1) == n &&
+                      scales.size(2) == k / 32 && out.size(0) == m && out.size(1) == groups &&
+                      out.size(2) == n,
+                  "Invalid packed Q8 shape/strides; K must be a multiple of 64");
+  torch::stable::accelerator::DeviceGuard guard(device);
+  raise_on_error(ci8_gguf_q8_packed_mm(x.data_ptr(), static_cast<int8_t*>(codes.data_ptr()),
+                                       scales.data_ptr(), out.data_ptr(), m, n, k, groups,
+                                       x.stride(0), x.stride(1), stream_for(device)));
+}
+
 }  // namespace
 
-// Schemas: csrc/bindings.cpp:594-595, 598, 603-607, 610; grouped_summed_mm has no
-// reference op.
+// Schemas: csrc/bindings.cpp:594-595, 598, 603-607, 610 and csrc/gguf_bindings.cpp:496;
+// grouped_summed_mm has no reference op.
 STABLE_TORCH_LIBRARY(consumer_int8, m) {
   m.def("fused_channel_mm(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor(a!) out, int schedule=0) -> ()");
   m.def("quantize_rows(Tensor input, Tensor(a!) codes, Tensor(b!) scales) -> ()");
@@ -253,6 +282,7 @@ STABLE_TORCH_LIBRARY(consumer_int8, m) {
   m.def("silu_mul(Tensor input, Tensor(a!) out) -> ()");
   m.def("silu_mul_quantize(Tensor input, Tensor(a!) codes, Tensor(b!) scales) -> ()");
   m.def("unpack_allspark(Tensor packed, Tensor packed_scales, Tensor(a!) weight, Tensor(b!) scales) -> ()");
+  m.def("gguf_q8_packed_mm(Tensor x, Tensor codes, Tensor scales, Tensor(a!) out) -> ()");
 }
 
 // HIP tensors carry the CUDA dispatch key in PyTorch-ROCm.
@@ -267,6 +297,7 @@ STABLE_TORCH_LIBRARY_IMPL(consumer_int8, CUDA, m) {
   m.impl("silu_mul", TORCH_BOX(&silu_mul));
   m.impl("silu_mul_quantize", TORCH_BOX(&silu_mul_quantize));
   m.impl("unpack_allspark", TORCH_BOX(&unpack_allspark));
+  m.impl("gguf_q8_packed_mm", TORCH_BOX(&gguf_q8_packed_mm));
 }
 
 extern "C" PyObject* PyInit__C() {

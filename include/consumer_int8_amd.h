@@ -27,6 +27,8 @@
  *                            its tiled variants :154-174, same contract)
  *   ci8_quantize_block32,    its two stages, benchmarks/cuda/q8_block_int8.cu:11-23 and
  *   ci8_q8_block_mm          :25-63, as separate entry points
+ *   ci8_gguf_q8_packed_mm    csrc/gguf_q8_packed.cu:279-285 (host launcher),
+ *                            csrc/gguf_bindings.cpp:135-171 (validation), schema :496
  */
 #ifndef CONSUMER_INT8_AMD_H
 #define CONSUMER_INT8_AMD_H
@@ -183,6 +185,24 @@ int ci8_q8_block_mm(const int8_t* a, const float* sa, const int8_t* w, const voi
  *           benchmarks/cuda/q8_block_int8.cu:142-152. */
 int ci8_q8_block_int8(const void* x, int8_t* a, float* sa, const int8_t* w, const void* sw,
                       void* y, int64_t m, int64_t n, int64_t k, void* stream);
+
+/* gguf_q8_packed_mm: grouped W8A16 with GGUF Q8_0 weights kept as their original codes
+ * and FP16 block scales. x BF16 [m, groups, k] addressed as x[i*x_row_stride +
+ * g*x_group_stride + t] (elements; k contiguous), codes INT8 [groups, n, k], scales
+ * FP16 [groups, n, k/32], out BF16 [m, groups, n] contiguous:
+ *   out[i, g, j] = bf16_rn(sum_t x[i, g, t] * bf16_rn(codes[g, j, t] * scales[g, j, t/32]))
+ * with FP32 accumulation in the kernel's own order. Requires k > 0, k % 64 == 0,
+ * m, n, groups >= 0, strides > 0 and multiples of 8, m <= 65535*32, groups <= 65535,
+ * k and n <= 2147483584; x and codes 16-byte and scales 4-byte aligned; out not
+ * overlapping an input (the reference rejects only identical pointers). An empty
+ * output (m, n or groups == 0) returns CI8_OK without a launch.
+ * Replaces: void gguf_q8_packed_mm(const void* x, const int8_t* q, const void* scales,
+ *           void* y, int m, int n, int k, int groups, int64_t xs, int64_t xg,
+ *           cudaStream_t), csrc/gguf_q8_packed.cu:279-285, with the checks of
+ *           csrc/gguf_bindings.cpp:135-171. */
+int ci8_gguf_q8_packed_mm(const void* x, const int8_t* codes, const void* scales, void* out,
+                          int64_t m, int64_t n, int64_t k, int64_t groups,
+                          int64_t x_row_stride, int64_t x_group_stride, void* stream);
 
 #ifdef __cplusplus
 }

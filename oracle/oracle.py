@@ -3,8 +3,9 @@
 This module restates, in numpy, the arithmetic of AppMana/consumer-int8-kernels for
 quantize_rows, quantize_grouped4096, fused/cutlass_channel_mm, channel_mm, channel_gemv,
 the channel weight encoding, the SwiGLU producers silu_mul / silu_mul_quantize, the
-AllSpark N32K16 weight layout (unpack_allspark, with its inverse packer) and the
-block-32 Q8_0 W8A8 path (quantize_block32, q8_block_mm). Only tests/, __graft_entry__.smoke() and bench.py's
+AllSpark N32K16 weight layout (unpack_allspark, with its inverse packer), the
+block-32 Q8_0 W8A8 path (quantize_block32, q8_block_mm) and the grouped GGUF Q8_0
+W8A16 product (gguf_q8_packed_mm, with pack_q8). Only tests/, __graft_entry__.smoke() and bench.py's
 cpu_baseline leg may import it, and only as the checker (or the timed CPU baseline);
 the product path never calls it and has no CPU fallback.
 
@@ -365,6 +366,60 @@ def q8_block_dense_reference(x_bits: np.ndarray, w: np.ndarray, sw_bits: np.ndar
     n, k = w.shape
     dense = w.astype(np.float64).reshape(n, k // 32, 32) * f16_to_f32(sw_bits)[..., None]
     return bf16_to_f32(x_bits).astype(np.float64) @ dense.reshape(n, k).T
+
+
+# ---------------------------------------------------------------- GGUF grouped Q8 W8A16
+
+def dequantize_q8_0(codes: np.ndarray, scale_bits: np.ndarray) -> np.ndarray:
+    """GGUF Q8_0 weights [..., K] as BF16 bits: bf16_rn(float(code) * float(scale)).
+
+    csrc/gguf_q8_packed.cu:208-210: the FP16 scale of each run of 32 codes widened to
+    FP32, multiplied by the signed code (exact in FP32: 8 x 11 significant bits) and
+    rounded once to BF16 (__floats2bfloat162_rn). scale_bits holds FP16 bit patterns
+    [..., K / 32].
+    """
+    codes = np.asarray(codes, dtype=np.int8)
+    *lead, k = codes.shape
+    blocks = codes.astype(np.float32).reshape(*lead, k // 32, 32)
+    prod = (blocks * f16_to_f32(scale_bits)[..., None]).astype(np.float32)
+    return f32_to_bf16(prod.reshape(*lead, k))
+
+
+def gguf_q8_packed_mm(x_bits, codes, scale_bits) -> tuple[np.ndarray, np.ndarray]:
+    """gguf_q8_packed_mm reference: (BF16 bits [M, G, N], float64 values [M, G, N]).
+
+    x [M, G, K] BF16 bits, codes [G, N, K] INT8, scale_bits [G, N, K / 32] FP16 bits.
+    out[m, g, :] = x[m, g, :] @ wq[g]^T with wq = dequantize_q8_0(codes, scales): the
+    product of csrc/gguf_q8_packed.cu:161-273 (BF16 tensor-core products with FP32
+    accumulation, :243, rounded to BF16 at :270), evaluated here in float64 and rounded
+    to BF16 -- the reference test's oracle (tests/test_gguf_q8.py:28-59, a float32 bmm of
+    the BF16 dense weights). The kernel's FP32 summation order is its own, so parity is
+    by tolerance: gguf_q8_abs_bound.
+    """
+    xf = bf16_to_f32(x_bits).astype(np.float64)
+    wq = bf16_to_f32(dequantize_q8_0(codes, scale_bits)).astype(np.float64)
+    exact = np.stack([xf[:, g, :] @ wq[g].T for g in range(wq.shape[0])], axis=1)
+    return f64_to_bf16(exact), exact
+
+
+def gguf_q8_abs_bound(x_bits, codes, scale_bits) -> np.ndarray:
+    """Worst-case FP32 summation error K * 2^-24 * sum_k |x * wq| per output [M, G, N]."""
+    xf = np.abs(bf16_to_f32(x_bits).astype(np.float64))
+    wq = np.abs(bf16_to_f32(dequantize_q8_0(codes, scale_bits)).astype(np.float64))
+    k = xf.shape[2]
+    return k * 2.0**-24 * np.stack([xf[:, g, :] @ wq[g].T for g in range(wq.shape[0])], axis=1)
+
+
+def pack_q8(raw: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Raw GGUF Q8_0 blocks [G, N, K/32, 34] (2-byte little-endian FP16 scale, then 32
+    INT8 codes) -> (codes INT8 [G, N, K], scales FP16 bits [G, N, K/32]), losslessly
+    (src/consumer_int8/gguf.py:79-96)."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    g, n, blocks, width = raw.shape
+    assert width == 34
+    scales = raw[..., :2].copy().view("<u2").reshape(g, n, blocks)
+    codes = raw[..., 2:].copy().view(np.int8).reshape(g, n, blocks * 32)
+    return codes, scales.astype(np.uint16)
 
 
 # ---------------------------------------------------------------- AllSpark N32K16

@@ -23,6 +23,7 @@ def test_header_declares_the_expected_entry_points():
         "ci8_fused_channel_mm", "ci8_cutlass_channel_mm", "ci8_channel_mm",
         "ci8_channel_gemv", "ci8_grouped_summed_mm", "ci8_silu_mul", "ci8_silu_mul_quantize",
         "ci8_unpack_allspark", "ci8_quantize_block32", "ci8_q8_block_mm", "ci8_q8_block_int8",
+        "ci8_gguf_q8_packed_mm",
     ])
 
 
@@ -197,6 +198,37 @@ def test_q8_block_rejections(lib):
            A.CI8_ERR_OVERLAP, "must not overlap")
 
 
+def test_gguf_q8_packed_rejections(lib):
+    """csrc/gguf_bindings.cpp:148-161 in order: shape/strides (K % 64, positive strides),
+    grid limits, copy alignment; then an empty output returns without a launch, and an
+    output overlapping an input is refused."""
+    from consumer_int8 import _abi as A
+
+    def call(x=FAKE, q=FAKE << 1, s=FAKE << 2, out=FAKE << 3, m=4, n=8, k=64, g=2,
+             xs=128, xg=64):
+        return lib.ci8_gguf_q8_packed_mm(x, q, s, out, m, n, k, g, xs, xg, None)
+
+    shape = "Invalid packed Q8 shape/strides; K must be a multiple of 64"
+    for bad in [dict(k=32), dict(k=96), dict(k=0), dict(m=-1), dict(n=-1), dict(g=-1),
+                dict(xs=0), dict(xg=-64)]:
+        expect(lib, call(**bad), A.CI8_ERR_GEOMETRY, shape)
+    for bad in [dict(m=65535 * 32 + 1), dict(g=65536), dict(n=2147483584 + 1)]:
+        expect(lib, call(**bad), A.CI8_ERR_TOO_LARGE, "Packed Q8 grid too large")
+    for bad in [dict(xs=132), dict(xg=68), dict(x=FAKE + 8), dict(q=(FAKE << 1) + 8),
+                dict(s=(FAKE << 2) + 2)]:
+        expect(lib, call(**bad), A.CI8_ERR_ALIGNMENT, "Packed Q8 copy alignment violation")
+    # checks precede the empty-output return, as in the reference
+    expect(lib, call(m=0, k=32), A.CI8_ERR_GEOMETRY, shape)
+    for empty in [dict(m=0), dict(n=0), dict(g=0)]:
+        assert call(**empty) == A.CI8_OK, A.last_error()
+    # extents that would overflow 64-bit offsets
+    expect(lib, call(m=65535 * 32, n=2147483584, g=65535), A.CI8_ERR_TOO_LARGE, "too large")
+    expect(lib, call(xs=1 << 60, m=64), A.CI8_ERR_TOO_LARGE, "too large")
+    for alias in [dict(out=FAKE), dict(out=FAKE << 1), dict(out=FAKE << 2),
+                  dict(out=FAKE + 200)]:
+        expect(lib, call(**alias), A.CI8_ERR_OVERLAP, "Packed Q8 output must not alias inputs")
+
+
 def test_torch_surface_matches_reference_schemas():
     import torch
 
@@ -214,10 +246,16 @@ def test_torch_surface_matches_reference_schemas():
         "silu_mul": "(Tensor input, Tensor(a!) out) -> ()",
         "silu_mul_quantize": "(Tensor input, Tensor(a!) codes, Tensor(b!) scales) -> ()",
         "unpack_allspark": "(Tensor packed, Tensor packed_scales, Tensor(a!) weight, Tensor(b!) scales) -> ()",
+        # csrc/gguf_bindings.cpp:496
+        "gguf_q8_packed_mm": "(Tensor x, Tensor codes, Tensor scales, Tensor(a!) out) -> ()",
     }
+    from consumer_int8 import gguf
+
+    assert gguf.q8_packed_mm is torch.ops.consumer_int8.gguf_q8_packed_mm
     for name, schema in expected.items():
-        handle = getattr(ops, name)
-        assert handle is getattr(torch.ops.consumer_int8, name)
+        handle = getattr(torch.ops.consumer_int8, name)
+        if hasattr(ops, name):
+            assert getattr(ops, name) is handle
         assert str(handle.default._schema) == f"consumer_int8::{name}{schema}"
 
 
@@ -255,3 +293,9 @@ def test_fake_tensor_registration():
         assert ops.unpack_allspark(packed, torch.empty(32, dtype=torch.bfloat16),
                                    torch.empty(16, 16, dtype=torch.int8),
                                    torch.empty(16, dtype=torch.bfloat16)) is None
+        from consumer_int8 import gguf
+
+        assert gguf.q8_packed_mm(torch.empty(3, 2, 64, dtype=torch.bfloat16),
+                                 torch.empty(2, 5, 64, dtype=torch.int8),
+                                 torch.empty(2, 5, 2, dtype=torch.float16),
+                                 torch.empty(3, 2, 5, dtype=torch.bfloat16)) is None

@@ -556,3 +556,79 @@ def test_q8_block_mm_matches_exact_rationals_and_the_reference_tolerance():
     assert np.all(np.abs(got - ref_bf16) <= 1e-5 + 0.008 * np.abs(ref_bf16))
     dense = O.q8_block_dense_reference(bits, w, sw)
     assert np.linalg.norm(got - dense) / np.linalg.norm(dense) < 0.015
+
+
+# ------------------------------------------------------------------ GGUF grouped Q8 W8A16
+
+def test_dequantize_q8_0_exact_rationals():
+    """bf16_rn(code * fp16 scale), per run of 32 codes: every code, FP16 normal,
+    subnormal, negative and zero scales, against Fraction arithmetic with one rounding."""
+    codes = np.arange(-128, 128, dtype=np.int32).astype(np.int8).reshape(2, 128)
+    scales = np.array([[1.0, -0.0999, 6.1e-5, 3e-7], [0.0, 65504.0, -2.5e-3, 1 / 3]],
+                      np.float16).view(np.uint16)
+    wq = O.dequantize_q8_0(codes, scales)
+    assert wq.shape == (2, 128) and wq.dtype == np.uint16
+    sf = scales.view(np.float16).astype(np.float64)
+    for r in range(2):
+        for t in range(128):
+            want = E.bf16(Fraction(int(codes[r, t])) * Fraction(float(sf[r, t // 32])))
+            assert int(wq[r, t]) == E.bf16_bits(float(want)), (r, t)
+    # grouped leading dimensions dequantize each [N, K] independently
+    g3 = np.stack([codes, -codes.astype(np.int16).clip(-128, 127).astype(np.int8), codes])
+    s3 = np.stack([scales, scales, scales[::-1]])
+    wq3 = O.dequantize_q8_0(g3, s3)
+    for g in range(3):
+        assert np.array_equal(wq3[g], O.dequantize_q8_0(g3[g], s3[g]))
+
+
+def test_gguf_q8_packed_mm_brute_force_per_group():
+    """Exact rational dot products per (row, group, channel) on a tiny grouped case, with
+    distinct groups so that a swapped row/group index or a transposed operand fails."""
+    rng = np.random.default_rng(95)
+    m, g, n, k = 2, 3, 4, 64
+    x = O.f32_to_bf16(rng.standard_normal((m, g, k)).astype(np.float32))
+    codes = rng.integers(-128, 128, (g, n, k)).astype(np.int8)
+    scales = (rng.random((g, n, k // 32)) * 0.1 * np.array([1, 10, 100])[:, None, None]
+              ).astype(np.float16).view(np.uint16)
+    out, exact_vals = O.gguf_q8_packed_mm(x, codes, scales)
+    assert out.shape == (m, g, n) and exact_vals.shape == (m, g, n)
+    xf = O.bf16_to_f32(x)
+    sf = scales.view(np.float16).astype(np.float64)
+    for i in range(m):
+        for gg in range(g):
+            for j in range(n):
+                dot = Fraction(0)
+                for t in range(k):
+                    wq = E.bf16(Fraction(int(codes[gg, j, t])) * Fraction(float(sf[gg, j, t // 32])))
+                    dot += Fraction(float(xf[i, gg, t])) * wq
+                assert abs(Fraction(exact_vals[i, gg, j]) - dot) <= abs(dot) * Fraction(1, 2**50) + Fraction(1, 2**120)
+                assert int(out[i, gg, j]) == E.bf16_bits(float(E.bf16(E.f32(Fraction(float(exact_vals[i, gg, j]))))))
+    bound = O.gguf_q8_abs_bound(x, codes, scales)
+    assert bound.shape == (m, g, n) and np.all(bound > 0)
+
+
+def test_gguf_q8_oracle_meets_the_reference_test():
+    """tests/test_gguf_q8.py:22-59 construction: raw blocks = FP16 scale bytes then 32
+    codes; pack_q8 recovers codes and scales; the oracle is within the reference's
+    relative-norm 0.001 of a float32 bmm of the BF16 dense weights."""
+    rng = np.random.default_rng(37)
+    groups, n, k, m = 3, 37, 128, 17
+    scales = (rng.random((groups, n, k // 32, 1)) * 0.1).astype(np.float16)
+    codes = rng.integers(-128, 128, (groups, n, k // 32, 32)).astype(np.int8)
+    raw = np.concatenate((scales.view(np.uint8), codes.view(np.uint8)), axis=-1)
+    assert raw.shape == (groups, n, k // 32, 34)
+    pc, ps = O.pack_q8(raw)
+    assert np.array_equal(pc, codes.reshape(groups, n, k))
+    assert np.array_equal(ps, scales.view(np.uint16).reshape(groups, n, k // 32))
+    # little-endian FP16 scale in the first two bytes of each block
+    assert ps[0, 0, 0] == int(raw[0, 0, 0, 0]) | (int(raw[0, 0, 0, 1]) << 8)
+    dense = O.f32_to_bf16((scales.astype(np.float32) * codes.astype(np.float32)).reshape(groups, n, k))
+    assert np.array_equal(dense, O.dequantize_q8_0(pc, ps))
+    x = O.f32_to_bf16(rng.standard_normal((m, groups, k)).astype(np.float32))
+    out, _ = O.gguf_q8_packed_mm(x, pc, ps)
+    xf = O.bf16_to_f32(x)
+    ref = np.stack([xf[:, g] @ O.bf16_to_f32(dense[g]).T for g in range(groups)], axis=1)
+    ref = O.bf16_to_f32(O.f32_to_bf16(ref.astype(np.float32))).astype(np.float64)
+    got = O.bf16_to_f32(out).astype(np.float64)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 0.001
+    assert np.all(np.isfinite(got)) and np.abs(got).max() > 0
