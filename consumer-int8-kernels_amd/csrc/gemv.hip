@@ -27,12 +27,15 @@
 //  * One barrier per stage. The ring has three slots, held in three separate LDS
 //    arrays so the compiler can see that the slot being read is not the slot an
 //    in-flight copy is writing.
-// For small batches (x[0:m, :] within 64 KiB of LDS: m <= 6 at K = 5120) a second kernel
-// copies all of x into LDS once and then lets every wave stream its W through a rolling
-// window of ten 64-byte blocks with no barriers at all, which removes the per-stage
-// lock-step of the ring. Up to 160 KiB of LDS (m <= 14 at K = 5120), a persistent form
-// of it runs one workgroup per CU that copies x once and walks its channel blocks.
-// Weight rows past N and K chunks past K read as zero through the buffer range check.
+// For K <= 8192 and 2 <= m <= 16, a balanced-span kernel (one 16-wave workgroup per
+// CU over an equal share of the channels, x fragments held in registers, W streamed one
+// block of 16 channels ahead) replaces the kernels below. At m = 1, and for longer K
+// while x[0:m, :] fits in 64 KiB of LDS, a second kernel copies all of x into LDS once
+// and then lets every wave stream its W through a rolling window of ten 64-byte blocks
+// with no barriers at all, which removes the per-stage lock-step of the ring. Up to
+// 160 KiB of LDS, a persistent form of it runs one workgroup per CU that copies x once
+// and walks its channel blocks; beyond that, the ring. Weight rows past N and K chunks
+// past K read as zero through the buffer range check.
 #include "ci8_device.h"
 #include "launch.h"
 
@@ -478,10 +481,169 @@ __global__ void __launch_bounds__(C::kThreads, C::kWavesPerEU) channel_gemv_pers
   waitcnt<vmcnt_imm(0)>();  // drain the trailing (out-of-range) loads before exit
 }
 
+// ---------------------------------------------------------------------------------
+// Balanced-span variant: one 16-wave workgroup per CU, x in registers.
+//
+// Workgroup b owns the channel span [b * span, (b + 1) * span) with span = ceil(N /
+// grid), so every CU streams the same number of weight bytes (N = 17408 on 256 CUs: 68
+// channels, 348 KiB each) and no CU waits on a second round. The span is walked in
+// blocks of 16 channels; the last block's rows past the span load nothing (range-checked
+// offsets) and are not stored. Wave r sums K range r (kSpb 64-element blocks at most);
+// its x fragments for that range (x[0:16, range] as MFMA B operands, rows past m zero)
+// are loaded once into kSpb * 8 registers and reused for every block, so x needs no
+// LDS and M = 16 costs what M = 1 does.
+//  * W streams one block ahead: after a slot's MFMAs, the wave issues that slot's load
+//    for the next block, and at the start of a block the next block's channel scale.
+//    Loads retire in issue order, so at slot s of block lb the loads issued after
+//    W(lb, s) are the rest of block lb, the scale of lb + 1 and the first s slots of lb
+//    + 1: vmcnt(kSpb) before a slot means its W has landed, and vmcnt(kSpb + 1) at the
+//    start of a block, after the next scale is issued, means this block's scale has.
+//    The prologue issues x, the scale of block 0 and W(0, *), which gives the same
+//    counts. The last block's loads for the block after it are out of range (no
+//    memory traffic) and are drained before exit.
+//  * Each block's 16 per-range partial sums go to LDS (kBatch blocks' worth); after
+//    every kBatch blocks and after the last, one barrier pair adds them in range order,
+//    rounds to BF16 and stores, so the waves synchronise once per kBatch blocks.
+template <int kSpb_>
+struct SpanConfig {
+  static constexpr int kS = 16;       // waves, one K range each
+  static constexpr int kSpb = kSpb_;  // 64-element K blocks per range
+  static constexpr int kBatch = 8;    // blocks per partial-sum reduction (128 KiB of LDS)
+  static constexpr int kThreads = 64 * kS;
+  static_assert(kSpb + 1 <= 63, "vmcnt holds 6 bits");
+};
+
+template <class C>
+__global__ void __launch_bounds__(C::kThreads) channel_gemv_span_kernel(
+    const uint16_t* __restrict__ x, const int8_t* __restrict__ w,
+    const uint16_t* __restrict__ scale, uint16_t* __restrict__ out, int m, int n, int k,
+    int span) {
+  __shared__ f32x4 partial[C::kBatch][C::kS][64];
+  const int c0 = int(blockIdx.x) * span;
+  if (c0 >= n) return;  // uniform over the workgroup
+  const int c_end = min(c0 + span, n);
+  const int nlocal = (c_end - c0 + 15) / 16;
+
+  const int lane = threadIdx.x & 63;
+  const int range = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row = lane & 15, group = lane >> 4;
+  const int kblocks = (k + 63) / 64;
+  const int range_len = (kblocks + C::kS - 1) / C::kS;  // <= kSpb (host-checked)
+  const int kb_first = range * range_len;
+  const int my_slots = max(0, min(kb_first + range_len, kblocks) - kb_first);
+
+  const auto w_rsrc = make_rsrc(w, uint32_t(n) * uint32_t(k));
+  const auto x_rsrc = make_rsrc(x, uint32_t(m) * uint32_t(k) * 2u);
+  const auto s_rsrc = make_rsrc(scale, uint32_t(n) * 2u);
+
+  // Byte offset of this lane's 16 codes of block lb, slot s (kOutOfRange: load zeros).
+  auto w_offset = [&](int lb, int s) __attribute__((always_inline)) {
+    const int channel = c0 + lb * 16 + row;
+    const int col = (kb_first + s) * 64 + group * 16;
+    const bool valid = channel < c_end && s < my_slots && col < k;
+    return valid ? uint32_t(channel) * uint32_t(k) + uint32_t(col) : kOutOfRange;
+  };
+  auto load_scale = [&](int lb) __attribute__((always_inline)) {
+    const int channel = c0 + lb * 16 + row;
+    return __builtin_amdgcn_raw_buffer_load_b16(
+        s_rsrc, channel < c_end ? uint32_t(channel) * 2u : kOutOfRange, 0, 0);
+  };
+
+  // x fragments: lane (row, group) holds x[row, kb * 64 + 16 * group + 8 * h + 0..7].
+  u32x4 xf[C::kSpb][2];
+#pragma unroll
+  for (int s = 0; s < C::kSpb; ++s) {
+    const int col = (kb_first + s) * 64 + group * 16;
+    const bool valid = row < m && s < my_slots && col < k;
+    const uint32_t base = uint32_t(row) * uint32_t(k) * 2u + uint32_t(col) * 2u;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      xf[s][h] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, valid ? base + 16u * h : kOutOfRange,
+                                                       0, 0));
+  }
+  uint32_t s_next = load_scale(0);
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 wv[C::kSpb];
+#pragma unroll
+  for (int s = 0; s < C::kSpb; ++s) {
+    wv[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(0, s), 0, 0));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // Adds the partials of local blocks [lb0, lb0 + count) and stores them.
+  auto reduce = [&](int lb0, int count) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+    workgroup_barrier();
+    for (int i = threadIdx.x; i < count * 256; i += C::kThreads) {
+      const int b = i >> 8, e = i & 3, l = (i >> 2) & 63;
+      const int out_row = l & 15;
+      const int out_col = c0 + (lb0 + b) * 16 + (l >> 4) * 4 + e;
+      if (out_row < m && out_col < c_end) {
+        float sum = partial[b][0][l][e];
+#pragma unroll
+        for (int v = 1; v < C::kS; ++v) sum += partial[b][v][l][e];
+        out[int64_t(out_row) * n + out_col] = uint16_t(f32_to_bf16(sum));
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+    workgroup_barrier();
+  };
+
+  for (int lb = 0; lb < nlocal; ++lb) {
+    const float sc = bf16_to_f32(s_next);
+    s_next = load_scale(lb + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    waitcnt<vmcnt_imm(C::kSpb + 1)>();  // the scale of block lb has landed
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < C::kSpb; ++s) {
+      waitcnt<vmcnt_imm(C::kSpb)>();  // W(lb, s) has landed
+      if (s < my_slots) {
+        const u32x4 wq = wv[s];
+        const u32x2 d0 = dequant4(wq[0], sc), d1 = dequant4(wq[1], sc);
+        const u32x2 d2 = dequant4(wq[2], sc), d3 = dequant4(wq[3], sc);
+        acc = mfma_bf16(u32x4{d0[0], d0[1], d1[0], d1[1]}, xf[s][0], acc);
+        acc = mfma_bf16(u32x4{d2[0], d2[1], d3[0], d3[1]}, xf[s][1], acc);
+      }
+      wv[s] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(lb + 1, s), 0, 0));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    partial[lb % C::kBatch][range][lane] = acc;
+    if (lb % C::kBatch == C::kBatch - 1 || lb + 1 == nlocal)  // uniform
+      reduce(lb / C::kBatch * C::kBatch, lb % C::kBatch + 1);
+  }
+  waitcnt<vmcnt_imm(0)>();  // drain the trailing (out-of-range) loads before exit
+}
+
+template <class C>
+hipError_t run_span(const void* x, const int8_t* w, const void* scale, void* out, int m, int n,
+                    int k, int cus, hipStream_t stream) {
+  const int grid = min(cus, (n + 15) / 16);
+  const int span = (n + grid - 1) / grid;
+  channel_gemv_span_kernel<C><<<grid, C::kThreads, 0, stream>>>(
+      static_cast<const uint16_t*>(x), w, static_cast<const uint16_t*>(scale),
+      static_cast<uint16_t*>(out), m, n, k, span);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale, void* out,
                                int m, int n, int k, hipStream_t stream) {
+  // K <= 8192 and m >= 2: the balanced-span kernel (measured on MI355X at K = 5120, N =
+  // 17408: 20.2 - 22.9 us over m = 2 .. 16, against 20.4 - 30.9 us for the kernels below).
+  // At m = 1 the resident kernel, whose 32 waves per CU request almost all of their
+  // weights at once, stays about 1 us ahead (19.2 against 20.2 us).
+  const int cus = device_cu_count();
+  const int range_len = ((k + 63) / 64 + 15) / 16;
+  if (cus > 0 && range_len <= 8 && m >= 2) {
+    if (range_len <= 2) return run_span<SpanConfig<2>>(x, w, scale, out, m, n, k, cus, stream);
+    if (range_len <= 4) return run_span<SpanConfig<4>>(x, w, scale, out, m, n, k, cus, stream);
+    if (range_len <= 5) return run_span<SpanConfig<5>>(x, w, scale, out, m, n, k, cus, stream);
+    return run_span<SpanConfig<8>>(x, w, scale, out, m, n, k, cus, stream);
+  }
   // Measured on MI355X at K=5120, N=17408: x resident in LDS with 8 K ranges per block of
   // 16 channels and a 10-block window wins while two workgroups fit on a CU (m <= 6:
   // 23.9 / 24.2 us at m = 5 / 6 against 25.2 / 25.4 us for the ring); with one per CU
@@ -510,7 +672,6 @@ hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale
   // 26 - 27 us for the ring).
   using P = ResidentConfig<16, 5, 4>;
   constexpr int kStaticLds = P::kS * 64 * 16;  // partial sums
-  const int cus = device_cu_count();
   if (lds + kStaticLds <= 160 * 1024 && cus > 0) {
     auto kernel = channel_gemv_persistent_kernel<P>;
     static std::atomic<bool> configured{false};

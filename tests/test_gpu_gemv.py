@@ -64,12 +64,29 @@ def test_decode_shape_full_size(ops, m):
 
 @pytest.mark.parametrize("m,n,k", [(12, 1000, 5104), (10, 4100, 5120), (14, 250, 5120),
                                    (9, 17, 8192), (10, 16 * 256 * 3 + 16, 5120),
-                                   (7, 300, 5120)])
-def test_persistent_batches_walk_their_channel_blocks(ops, m, n, k):
-    """Batches whose x takes more than 64 KiB of LDS (7 <= m <= 14 at K = 5120) run one
-    workgroup per CU that walks channel blocks blockIdx.x, blockIdx.x + grid, ...: fewer
-    blocks than CUs, more (unevenly shared), a partial last block and a K tail."""
+                                   (7, 300, 5120), (16, 36869, 2048), (5, 2000, 4096),
+                                   (2, 16 * 256 * 9 + 5, 1024), (1, 17408, 5120)])
+def test_balanced_spans(ops, m, n, k):
+    """K <= 8192 (m >= 2) runs one workgroup per CU over equal channel spans (N = 17408:
+    68 per CU): fewer channels than CUs x 16, spans that end inside a block of 16, more
+    than 8 blocks per span (two partial-sum batches), every x-register configuration (K
+    ranges of 2, 4, 5 and 8 blocks of 64) and a K tail; m = 1 takes the resident kernel."""
     rng = np.random.default_rng(m * 7 + n + k)
+    x_bits = randn_bf16(rng, (m, k))
+    w = rng.integers(-128, 128, (n, k)).astype(np.int8)
+    s_bits = O.f32_to_bf16(rng.uniform(1e-3, 1e-2, n).astype(np.float32))
+    out = torch.full((m, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+    ops.channel_gemv(to_dev(x_bits), to_dev(w), to_dev(s_bits), out)
+    torch.cuda.synchronize()
+    check_gemv(bf16_bits(out), x_bits, w, s_bits)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 5000, 16384), (5, 600, 12288), (8, 300, 12288),
+                                   (16, 70, 9216)])
+def test_long_k_kernels(ops, m, n, k):
+    """K > 8192: x resident in LDS (m * K * 2 <= 64 KiB), the persistent walk over channel
+    blocks (up to 144 KiB) and the LDS ring beyond."""
+    rng = np.random.default_rng(m * 5 + n + k)
     x_bits = randn_bf16(rng, (m, k))
     w = rng.integers(-128, 128, (n, k)).astype(np.int8)
     s_bits = O.f32_to_bf16(rng.uniform(1e-3, 1e-2, n).astype(np.float32))
