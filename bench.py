@@ -15,8 +15,9 @@ under a full-chip pure-MFMA loop, with the dense INT8 peak at that measured cloc
 timed as in the reference microbenchmark (graph replays of 10 launches, median); extra roofline lines for the quantizer, the W8A16
 GEMV, the grouped summed GEMM, the biased-UINT8 down
 projection with its SwiGLU activation producers (silu_mul_quantize,
-silu_mul) and the AllSpark weight restore (unpack_allspark), and the small quantize +
-GEMM pass (configs[0]); and
+silu_mul), the AllSpark weight restore (unpack_allspark), the block-32 Q8_0 W8A8 GEMM,
+the GGUF Q8_0 grouped W8A16 op (gguf_q8_packed_mm) and the small quantize + GEMM pass
+(configs[0]); and
 `cpu_baseline`, the reference's torch CPU math for the same step on a bounded row slice,
 on this host's cores.
 
@@ -50,6 +51,7 @@ GEMM_OPS = 2 * M * N * K  # 730,144,440,320
 QUANT_BYTES = 3 * M * K + 4 * M  # BF16 read + INT8 write + FP32 scales
 PEAK_INT8_TOPS = 256 * 2.4e9 * 8192 / 1e12  # 5033.2: 256 CUs x 2.4 GHz x 8192 op/clk/CU
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0  # dense BF16 MFMA
 GEMV_K, GEMV_N = 5120, 17408
 # HBM-side bytes per GEMM launch at this shape, from two rocprofv3 --pmc runs of this
 # script (FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00; the factors make a plain 512 MiB copy
@@ -490,6 +492,38 @@ def main() -> int:
                             "valu_frac": round(rescale / valu_peak, 4),
                             "mean_us": round(mean_us, 2), "ops": ops_q}
         del xq, wq, swq, aq, saq, yq
+        # GGUF Q8_0 grouped W8A16 (gguf_q8_packed_mm) at N = K = 4096, one group, rows as
+        # in the reference harness (benchmarks/benchmark_gguf_q8.py:477): 16 weight copies
+        # (285 MB) rotate so that the decode row count streams from HBM; 2048 rows are
+        # bounded by the dense BF16 MFMA peak.
+        from consumer_int8 import gguf
+
+        NG, KG = 4096, 4096
+        gq = [torch.randint(-128, 128, (1, NG, KG), generator=gen, device="cuda", dtype=torch.int8)
+              for _ in range(16)]
+        gs = (torch.rand(1, NG, KG // 32, generator=gen, device="cuda") * 0.01).half()
+        for mg in (16, 2048):
+            xg = torch.randn(mg, 1, KG, generator=gen, device="cuda").to(torch.bfloat16)
+            og = torch.empty(mg, 1, NG, device="cuda", dtype=torch.bfloat16)
+            calls = [lambda i=i: gguf.q8_packed_mm(xg, gq[i], gs, og) for i in range(16)]
+            for c in calls:
+                c()
+            mean_us, _ = time_kernel(torch, calls, 4)
+            bg = NG * KG + NG * KG // 16 + 2 * mg * KG + 2 * mg * NG
+            fg = 2 * mg * NG * KG
+            if mg <= 16:
+                gbs = bg / (mean_us * 1e-6) / 1e9
+                extras[f"gguf_q8_packed_m{mg}"] = {
+                    "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": round(gbs / PEAK_HBM_GBS, 4), "mean_us": round(mean_us, 2), "bytes": bg}
+            else:
+                tf = fg / (mean_us * 1e-6) / 1e12
+                extras[f"gguf_q8_packed_m{mg}"] = {
+                    "bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                    "mean_us": round(mean_us, 2), "flops": fg}
+            del xg, og
+        del gq, gs
         # quantize_rows + fused_channel_mm at M=128, K=4096, N=4096; AI 234
         # op/B is below the ridge, so this small case is bounded by HBM (bytes below).
         M1, K1, N1 = 128, 4096, 4096

@@ -37,9 +37,13 @@
 // A W wave has 7 copies per stage against an A wave's 8; its eighth reads nothing into a
 // junk KiB, which keeps the copy sequence identical and branch-free.
 //
-// MFMA lane layouts are those of gemm.hip: the MFMA computes D[n][m] = W . A^T, within a
-// 128-byte stage lane group g (lane / 16) reads logical chunk 2g + h in K-step h, and
-// LDS rows hold their 16-byte chunks XOR-swizzled by row % 8.
+// MFMA lane layouts: the MFMA computes D[n][m] = W . A^T; within a 128-byte stage, lane
+// group g (lane / 16) reads logical chunk 4h + g in K-step h (A and W alike, so the
+// exact INT32 sums are those of any other K order), and LDS rows hold their 16-byte
+// chunks XOR-swizzled by row % 8. With this order the 16 lanes of a group read one
+// chunk column of 16 rows and a fragment read has no bank conflicts (measured on
+// MI355X: the order 2g + h, where the four groups read every other chunk, stalls each
+// 1 KiB read about 4 cycles on bank conflicts, a quarter of the kernel's LDS time).
 #include "ci8_device.h"
 #include "launch.h"
 
@@ -151,12 +155,12 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
                                              off, k0, 0, 0);
   };
 
-  // Fragments: row (lane % 16) of each 16-row block at logical chunk 2 * (lane / 16) + h.
+  // Fragments: row (lane % 16) of each 16-row block at logical chunk 4h + lane / 16.
   const int f_row = lane & 15, f_group = lane >> 4;
   int a_base[2], w_base[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int swz = (((2 * f_group + h) ^ (f_row & 7)) * 16);
+    const int swz = (((4 * h + f_group) ^ (f_row & 7)) * 16);
     a_base[h] = (wm * 64 + f_row) * C::BK + swz;
     w_base[h] = C::kWBase + (group * 112 + f_row) * C::BK + swz;
   }
