@@ -5,7 +5,14 @@
 //
 // the arithmetic of csrc/fused_mm.cu:24-38 (and of gemm.hip, bit for bit).
 //
-// Tile 256 (m) x 224 (n) per workgroup of eight waves. Wave w owns rows 64 * (w % 4)
+// Persistent: one workgroup of eight waves per CU walks the 256 (m) x 224 (n) output
+// tiles b, b + grid, ... (grid = CU count). Between two tiles, the next tile's first
+// copies (A(0), W(0), W(1)) go out before this tile's epilogue, which then runs through
+// the one ring slot those copies do not use, so the operand latency of a tile start
+// hides behind the previous tile's stores (measured on MI355X at configs[2]: 281.6 ->
+// 277.7 us together with issuing no copies past a tile's last stage).
+//
+// Within a tile, wave w owns rows 64 * (w % 4)
 // and columns 112 * (w / 4) of the tile, as 4 x 7 blocks of v_mfma_i32_16x16x64_i8
 // accumulators (112 registers). Waves w and w + 4 share SIMD w % 4. The waves of group
 // g = w / 4 alternate between a memory phase (read the stage's 22 MFMA fragments from
@@ -44,6 +51,8 @@
 // chunk column of 16 rows and a fragment read has no bank conflicts (measured on
 // MI355X: the order 2g + h, where the four groups read every other chunk, stalls each
 // 1 KiB read about 4 cycles on bank conflicts, a quarter of the kernel's LDS time).
+#include <type_traits>
+
 #include "ci8_device.h"
 #include "launch.h"
 
@@ -70,13 +79,13 @@ struct PPConfig {
   // stride of 240 bytes (60 dwords: 16 rows written by one ds_write_b64 start in
   // distinct banks).
   static constexpr int kEpiRowBytes = (BN / 2) * 2 + 16;
-  static constexpr int kEpiWaveBytes = (BM / WM) * kEpiRowBytes;
-  static constexpr int kLdsBytes =
-      kRingBytes > kWaves * kEpiWaveBytes ? kRingBytes : kWaves * kEpiWaveBytes;
+  static constexpr int kEpiPassBytes = 16 * kEpiRowBytes;  // one 16-row block per wave
+  static constexpr int kLdsBytes = kRingBytes;
   static constexpr int GROUP_M = 8;
   static_assert(kCopies * WM == kABlocks && (kCopies - 1) * WM == kWBlocks, "copies");
   static_assert(3 * (kCopies - 1) < 2 * (TM + TN), "copies fit between the fragment reads");
   static_assert(kLdsBytes <= 160 * 1024, "LDS");
+  static_assert(kWaves * kEpiPassBytes <= kAStage, "epilogue passes fit in A slot 1");
 };
 
 __device__ __forceinline__ i32x4 lds16(const char __attribute__((address_space(3)))* p) {
@@ -104,23 +113,26 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
   const int wm = wave % C::WM, group = wave / C::WM;
   const bool copies_a = group == 0;
 
-  // Workgroup -> tile: undo the round-robin dealing over the 8 XCDs, then a grouped
-  // raster of GROUP_M m tiles, so tiles that run together on one XCD share panels.
+  // Work item -> tile: items are dealt to the 8 XCDs round-robin (workgroup b runs on
+  // XCD b % 8 and takes items b, b + grid, ...; the grid is a multiple of 8 when it
+  // fills the chip), so map the items of each XCD to a contiguous range of a grouped
+  // raster of GROUP_M m tiles: tiles that run together on one XCD share panels in its L2.
   const int tiles_n = (n + C::BN - 1) / C::BN;
   const int tiles_m = (m + C::BM - 1) / C::BM;
-  const int blocks = tiles_n * tiles_m;
-  int logical = blockIdx.x;
-  {
-    const int per = blocks / kXcds, extra = blocks % kXcds;
-    const int xcd = logical % kXcds, idx = logical / kXcds;
-    logical = (xcd < extra ? xcd * (per + 1) : extra * (per + 1) + (xcd - extra) * per) + idx;
-  }
-  const int group_span = C::GROUP_M * tiles_n;
-  const int first_m = (logical / group_span) * C::GROUP_M;
-  const int group_rows = min(tiles_m - first_m, C::GROUP_M);
-  const int tile_m = first_m + (logical % group_span) % group_rows;
-  const int tile_n = (logical % group_span) / group_rows;
-  const int m0 = tile_m * C::BM, n0 = tile_n * C::BN;
+  const int tiles = tiles_n * tiles_m;
+  const int grid = int(gridDim.x);
+  const int my_tiles = (tiles - int(blockIdx.x) + grid - 1) / grid;
+  auto tile_of = [&] __device__(int item, int& m0, int& n0) __attribute__((always_inline)) {
+    const int per = tiles / kXcds, extra = tiles % kXcds;
+    const int xcd = item % kXcds, idx = item / kXcds;
+    const int logical =
+        (xcd < extra ? xcd * (per + 1) : extra * (per + 1) + (xcd - extra) * per) + idx;
+    const int group_span = C::GROUP_M * tiles_n;
+    const int first_m = (logical / group_span) * C::GROUP_M;
+    const int group_rows = min(tiles_m - first_m, C::GROUP_M);
+    m0 = (first_m + (logical % group_span) % group_rows) * C::BM;
+    n0 = ((logical % group_span) / group_rows) * C::BN;
+  };
 
   const auto a_rsrc = make_rsrc(a, uint32_t(m) * uint32_t(k));
   const auto w_rsrc = make_rsrc(w, uint32_t(n) * uint32_t(k));
@@ -129,30 +141,42 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
 
   // Copy i of a wave brings block b = 4i + wave % 4 of its operand's stage (8 rows x 128
   // bytes): lane -> row 8b + lane / 8, LDS chunk slot lane % 8 holding logical chunk
-  // slot ^ (row % 8). The stage's K offset goes in soffset.
+  // slot ^ (row % 8). The stage's K offset goes in soffset; the per-lane row offsets
+  // depend on the tile and are set when a tile's first copies are issued.
   const int sub = wave % C::WM;
   const int c_row = lane >> 3;
   const int c_chunk = (lane & 7) ^ c_row;
   uint32_t c_off[C::kCopies];
+  auto set_copy_tile = [&] __device__(int m0, int n0) __attribute__((always_inline)) {
 #pragma unroll
-  for (int i = 0; i < C::kCopies; ++i) {
-    const int row = (copies_a ? m0 : n0) + (i * C::WM + sub) * 8 + c_row;
-    const bool valid = (copies_a || i < C::kCopies - 1) && row < (copies_a ? m : n);
-    c_off[i] = valid ? uint32_t(row) * uint32_t(k) + uint32_t(c_chunk * 16) : kOutOfRange;
-  }
+    for (int i = 0; i < C::kCopies; ++i) {
+      const int row = (copies_a ? m0 : n0) + (i * C::WM + sub) * 8 + c_row;
+      const bool valid = (copies_a || i < C::kCopies - 1) && row < (copies_a ? m : n);
+      c_off[i] = valid ? uint32_t(row) * uint32_t(k) + uint32_t(c_chunk * 16) : kOutOfRange;
+    }
+  };
   // LDS destination of copy i into ring slot `slot`: c_dst0 + slot * c_stride + 4096 i
   // (integer arithmetic on wave-uniform values), except a W wave's eighth (junk KiB).
   const int c_dst0 = (copies_a ? 0 : C::kWBase) + sub * 1024;
   const int c_stride = copies_a ? C::kAStage : C::kWStage;
-  // A copy of stage t < 0 reads nothing (out of range), into the free slot.
   auto copy = [&] __device__(int dst, int t, int i) __attribute__((always_inline)) {
     int to = dst + i * C::WM * 1024;
     if (i == C::kCopies - 1) to = copies_a ? to : C::kJunk;
-    const int k0 = t < 0 ? 0 : t * C::BK;
-    uint32_t off = t < 0 ? kOutOfRange : c_off[i];
+    const int k0 = t * C::BK;
+    uint32_t off = c_off[i];
     if (!kExactK && off != kOutOfRange && k0 + c_chunk * 16 >= k) off = kOutOfRange;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(c_rsrc, reinterpret_cast<lds_void*>(lds + to), 16,
                                              off, k0, 0, 0);
+  };
+  // A tile's first copies: A(0) (group 0) into A slot 0, W(0) and W(1) (group 1) into
+  // W slots 0 and 1.
+  auto first_copies = [&] __device__() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < C::kCopies; ++i) copy(c_dst0, 0, i);
+    if (!copies_a && 1 < ns) {
+#pragma unroll
+      for (int i = 0; i < C::kCopies; ++i) copy(c_dst0 + c_stride, 1, i);
+    }
   };
 
   // Fragments: row (lane % 16) of each 16-row block at logical chunk 4h + lane / 16.
@@ -166,9 +190,11 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
   }
   i32x4 af[2][C::TM], wf[2][C::TN];
   // Memory phase: the 22 fragments of the stage in A slot a_slot and W slot w_slot, with
-  // this wave's 8 copies of stage copy_t into `dst` after fragment reads 0, 3, ..., 21.
-  auto memory = [&] __device__(int a_slot, int w_slot, int dst, int copy_t)
+  // (kCopy) this wave's 8 copies of stage copy_t into `dst` after fragment reads 0, 3,
+  // ..., 21. Stages past the end are not copied at all.
+  auto memory = [&] __device__(int a_slot, int w_slot, int dst, int copy_t, auto with_copies)
                     __attribute__((always_inline)) {
+    constexpr bool kCopy = decltype(with_copies)::value;
     const auto* as = lds + a_slot * C::kAStage;
     const auto* ws = lds + w_slot * C::kWStage;
 #pragma unroll
@@ -178,16 +204,13 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
         af[h][r] = lds16(as + a_base[h] + r * 16 * C::BK);
       else
         wf[h][r - C::TM] = lds16(ws + w_base[h] + (r - C::TM) * 16 * C::BK);
-      if (q % 3 == 0) copy(dst, copy_t, q / 3);
+      if constexpr (kCopy)
+        if (q % 3 == 0) copy(dst, copy_t, q / 3);
     }
     __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
   };
 
   i32x4 acc[C::TM][C::TN];
-#pragma unroll
-  for (int j = 0; j < C::TM; ++j)
-#pragma unroll
-    for (int i = 0; i < C::TN; ++i) acc[j][i] = i32x4{0, 0, 0, 0};
   auto compute = [&] __device__() __attribute__((always_inline)) {
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -200,93 +223,129 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
     __builtin_amdgcn_s_setprio(0);
   };
 
-  // Prologue: A(0) (group 0), W(0) and W(1) (group 1) in place for everyone.
-#pragma unroll
-  for (int i = 0; i < C::kCopies; ++i) copy(c_dst0, 0, i);
-  if (!copies_a && 1 < ns) {
-#pragma unroll
-    for (int i = 0; i < C::kCopies; ++i) copy(c_dst0 + c_stride, 1, i);
-  }
+  if (my_tiles <= 0) return;  // uniform over the workgroup
+  int m0, n0;
+  tile_of(int(blockIdx.x), m0, n0);
+  set_copy_tile(m0, n0);
+  first_copies();
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   barrier_fenced();
 
-  // Stage t: group 0 copies A(t + 1) (into A slot (t + 1) % 2), group 1 W(t + 2) (into W
-  // slot (t + 2) % 3); copies past the last stage read nothing into that free slot.
-  int w_slot = 0;   // t % 3
-  int cw_slot = 2;  // (t + 2) % 3
-  const int lead = copies_a ? 1 : 2;
-  if (group == 1) barrier_fenced();  // phase 0 is group 0's first memory phase
-  for (int t = 0; t < ns; ++t) {
-    const int copy_t = t + lead < ns ? t + lead : -1;
-    const int dst = c_dst0 + (copies_a ? (t + 1) & 1 : cw_slot) * c_stride;
-    memory(t & 1, w_slot, dst, copy_t);
-    // Group 1: W(t + 1) landed (W(t + 2), just issued, may be in flight).
-    if (group == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(C::kCopies));
-    barrier_fenced();
-    compute();
-    // Group 0: A(t + 1), issued in the memory phase, landed.
-    if (group == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    barrier_fenced();
-    w_slot = w_slot == 2 ? 0 : w_slot + 1;
-    cw_slot = cw_slot == 2 ? 0 : cw_slot + 1;
-  }
-  if (group == 0) barrier_fenced();  // phase 2 ns: group 1's last compute phase
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // copies past the end, into free slots
-  barrier_fenced();                          // every wave's copies landed: ring is free
-
-  // Epilogue through LDS: the wave's 64 x 112 BF16 results go to its own region in the
-  // MFMA layout and come back as 16-byte row chunks, so each store instruction writes
-  // whole 224-byte row pieces (14 lanes per row).
-  const int row0 = m0 + wm * 64;
-  const int col0 = n0 + group * 112;
-  float rs[C::TM];
+  for (int r = 0; r < my_tiles; ++r) {
+    // This tile's row and channel scales, loaded now (older than any copy of the tile,
+    // so the waits of the K loop cover them).
+    float rs[C::TM];
+    u32x2 s2[C::TN];
+    {
+      const int row0 = m0 + wm * 64, col0 = n0 + group * 112;
 #pragma unroll
-  for (int j = 0; j < C::TM; ++j) {
-    const int row = row0 + j * 16 + f_row;
-    rs[j] = row < m ? sa[row] : 0.f;
-  }
-  u32x2 s2[C::TN];
-#pragma unroll
-  for (int i = 0; i < C::TN; ++i) {
-    const int col = col0 + i * 16 + f_group * 4;
-    s2[i] = col < n ? *reinterpret_cast<const u32x2*>(sw + col) : u32x2{0, 0};
-  }
-  auto* region = lds + wave * C::kEpiWaveBytes;
-#pragma unroll
-  for (int j = 0; j < C::TM; ++j) {
-    auto* rbase = region + (j * 16 + f_row) * C::kEpiRowBytes + f_group * 8;
-#pragma unroll
-    for (int i = 0; i < C::TN; ++i) {
-      float v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t bits = (s2[i][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-        v[e] = (float(acc[j][i][e]) * rs[j]) * bf16_to_f32(bits);
+      for (int j = 0; j < C::TM; ++j) {
+        const int row = row0 + j * 16 + f_row;
+        rs[j] = row < m ? sa[row] : 0.f;
       }
-      *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(rbase + i * 32) =
-          u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+#pragma unroll
+      for (int i = 0; i < C::TN; ++i) {
+        const int col = col0 + i * 16 + f_group * 4;
+        s2[i] = col < n ? *reinterpret_cast<const u32x2*>(sw + col) : u32x2{0, 0};
+      }
     }
-  }
-  // One wave's LDS operations complete in order; the wait only orders the reads after
-  // every lane's writes for the compiler.
-  __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
-  __builtin_amdgcn_wave_barrier();
-  constexpr int kChunks = 112 / 8;  // 16-byte chunks per output row piece
-  const bool full = out16 && row0 + 64 <= m && col0 + 112 <= n && (n % 8) == 0;
 #pragma unroll
-  for (int it = 0; it < kChunks; ++it) {
-    const int q = it * 64 + lane;
-    const int row = q / kChunks, chunk = q % kChunks;
-    const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
-        region + row * C::kEpiRowBytes + chunk * 16);
-    const int grow = row0 + row, gcol = col0 + chunk * 8;
-    uint16_t* dst = out + int64_t(grow) * n + gcol;
-    if (full) {
-      *reinterpret_cast<u32x4*>(dst) = v;
-    } else if (grow < m) {
+    for (int j = 0; j < C::TM; ++j)
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (gcol + e < n) dst[e] = uint16_t(v[e >> 1] >> (16 * (e & 1)));
+      for (int i = 0; i < C::TN; ++i) acc[j][i] = i32x4{0, 0, 0, 0};
+
+    // Stage t: group 0 copies A(t + 1) (into A slot (t + 1) % 2), group 1 W(t + 2) (into
+    // W slot (t + 2) % 3). The last stages, with nothing left to copy, issue no copies,
+    // and group 1 then waits for all of its copies instead of all but the newest stage's.
+    int w_slot = 0;   // t % 3
+    int cw_slot = 2;  // (t + 2) % 3
+    const int lead = copies_a ? 1 : 2;
+    if (group == 1) barrier_fenced();  // phase 0 is group 0's first memory phase
+    for (int t = 0; t < ns; ++t) {
+      const int copy_t = t + lead;
+      const int dst = c_dst0 + (copies_a ? (t + 1) & 1 : cw_slot) * c_stride;
+      if (copy_t < ns) {  // uniform over the wave
+        memory(t & 1, w_slot, dst, copy_t, std::true_type{});
+        // Group 1: W(t + 1) landed (W(t + 2), just issued, may be in flight).
+        if (group == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(C::kCopies));
+      } else {
+        memory(t & 1, w_slot, dst, copy_t, std::false_type{});
+        if (group == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      }
+      barrier_fenced();
+      compute();
+      // Group 0: A(t + 1), issued in the memory phase, landed.
+      if (group == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      barrier_fenced();
+      w_slot = w_slot == 2 ? 0 : w_slot + 1;
+      cw_slot = cw_slot == 2 ? 0 : cw_slot + 1;
+    }
+    if (group == 0) barrier_fenced();  // phase 2 ns: group 1's last compute phase
+    barrier_fenced();                  // every wave is past its last fragment reads
+
+    // The next tile's first copies go out now, into A slot 0 and W slots 0 and 1, and
+    // land while this tile's results are stored through A slot 1.
+    const int tile_m0 = m0, tile_n0 = n0;
+    const bool more = r + 1 < my_tiles;
+    if (more) {
+      tile_of(int(blockIdx.x) + (r + 1) * grid, m0, n0);
+      set_copy_tile(m0, n0);
+      first_copies();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+
+    // Epilogue through LDS, 16 rows of the wave's 64 at a time: the 16 x 112 BF16
+    // results of row block j go to the wave's 3840-byte region of A slot 1 in the MFMA
+    // layout and come back as 16-byte row chunks, so each store instruction writes whole
+    // 224-byte row pieces (14 lanes per row).
+    const int row0 = tile_m0 + wm * 64;
+    const int col0 = tile_n0 + group * 112;
+    auto* region = lds + C::kAStage + wave * C::kEpiPassBytes;
+    constexpr int kChunks = 112 / 8;  // 16-byte chunks per output row piece
+    const bool full = out16 && row0 + 64 <= m && col0 + 112 <= n && (n % 8) == 0;
+#pragma unroll
+    for (int j = 0; j < C::TM; ++j) {
+      auto* rbase = region + f_row * C::kEpiRowBytes + f_group * 8;
+#pragma unroll
+      for (int i = 0; i < C::TN; ++i) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t bits = (s2[i][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+          v[e] = (float(acc[j][i][e]) * rs[j]) * bf16_to_f32(bits);
+        }
+        *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(rbase + i * 32) =
+            u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+      }
+      // One wave's LDS operations complete in order; the wait only orders the reads
+      // after every lane's writes for the compiler.
+      __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int it = 0; it < (16 * kChunks + 63) / 64; ++it) {
+        const int q = it * 64 + lane;
+        if (q >= 16 * kChunks) break;
+        const int row = q / kChunks, chunk = q % kChunks;
+        const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+            region + row * C::kEpiRowBytes + chunk * 16);
+        const int grow = row0 + j * 16 + row, gcol = col0 + chunk * 8;
+        uint16_t* dst = out + int64_t(grow) * n + gcol;
+        if (full) {
+          *reinterpret_cast<u32x4*>(dst) = v;
+        } else if (grow < m) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (gcol + e < n) dst[e] = uint16_t(v[e >> 1] >> (16 * (e & 1)));
+        }
+      }
+      // The next row block's writes reuse the region after these reads.
+      __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+      __builtin_amdgcn_wave_barrier();
+    }
+    if (more) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the next tile's first copies landed
+      barrier_fenced();                          // every wave's, and A slot 1 is free
     }
   }
 }
@@ -298,21 +357,23 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
 hipError_t launch_pp_gemm(const int8_t* a, const int8_t* w, const float* sa, const void* sw,
                           void* out, int m, int n, int k, hipStream_t stream) {
   using C = PPConfig;
-  const int blocks = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
+  const int tiles = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
+  const int cus = device_cu_count();
+  const int grid = cus > 0 && cus < tiles ? cus : tiles;  // one workgroup per CU
   const bool out16 = (reinterpret_cast<uintptr_t>(out) & 15) == 0;
   if (k % C::BK == 0) {
     auto kernel = pp_gemm_kernel<true>;
     static std::atomic<bool> configured{false};
     if (const hipError_t e = raise_lds_limit_once(kernel, C::kLdsBytes, configured); e != hipSuccess)
       return e;
-    kernel<<<blocks, C::kThreads, C::kLdsBytes, stream>>>(
+    kernel<<<grid, C::kThreads, C::kLdsBytes, stream>>>(
         a, w, sa, static_cast<const uint16_t*>(sw), static_cast<uint16_t*>(out), m, n, k, out16);
   } else {
     auto kernel = pp_gemm_kernel<false>;
     static std::atomic<bool> configured{false};
     if (const hipError_t e = raise_lds_limit_once(kernel, C::kLdsBytes, configured); e != hipSuccess)
       return e;
-    kernel<<<blocks, C::kThreads, C::kLdsBytes, stream>>>(
+    kernel<<<grid, C::kThreads, C::kLdsBytes, stream>>>(
         a, w, sa, static_cast<const uint16_t*>(sw), static_cast<uint16_t*>(out), m, n, k, out16);
   }
   return hipGetLastError();
