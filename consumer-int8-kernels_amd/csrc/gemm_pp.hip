@@ -3,7 +3,9 @@
 //   out[m, n] = bf16_rn( fl( fl( float_rn(acc[m, n]) * sa[m] ) * float(sw[n]) ) )
 //   acc[m, n] = sum_k a[m, k] * w[n, k]            (exact INT32)
 //
-// the arithmetic of csrc/fused_mm.cu:24-38 (and of gemm.hip, bit for bit).
+// the arithmetic of csrc/fused_mm.cu:24-38 (and of gemm.hip, bit for bit). Biased UINT8
+// weights (channel_mm, code + 128) are turned into the signed codes in registers, one XOR
+// per four bytes after each W fragment read.
 //
 // Persistent: one workgroup of eight waves per CU walks the 256 (m) x 224 (n) output
 // tiles b, b + grid, ... (grid = CU count). Between two tiles, the next tile's first
@@ -99,7 +101,7 @@ __device__ __forceinline__ void barrier_fenced() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool kExactK>
+template <bool kExactK, WeightCode kCode>
 __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
     const int8_t* __restrict__ a, const int8_t* __restrict__ w, const float* __restrict__ sa,
     const uint16_t* __restrict__ sw, uint16_t* __restrict__ out, int m, int n, int k,
@@ -208,6 +210,13 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
         if (q % 3 == 0) copy(dst, copy_t, q / 3);
     }
     __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+    if constexpr (kCode == WeightCode::kBiasedU8) {
+      // Biased UINT8 codes (code + 128) -> signed INT8 codes: flip each byte's top bit.
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < C::TN; ++i) wf[h][i] ^= int(0x80808080u);
+    }
   };
 
   i32x4 acc[C::TM][C::TN];
@@ -354,29 +363,28 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
 
 // Requires a and w 16-byte aligned, sw 8-byte aligned and n % 4 == 0 (the fused op's
 // contract); out needs 2-byte alignment (16-byte aligned rows take 16-byte stores).
-hipError_t launch_pp_gemm(const int8_t* a, const int8_t* w, const float* sa, const void* sw,
-                          void* out, int m, int n, int k, hipStream_t stream) {
+hipError_t launch_pp_gemm(const int8_t* a, const void* w, WeightCode code, const float* sa,
+                          const void* sw, void* out, int m, int n, int k, hipStream_t stream) {
   using C = PPConfig;
   const int tiles = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
   const int cus = device_cu_count();
   const int grid = cus > 0 && cus < tiles ? cus : tiles;  // one workgroup per CU
   const bool out16 = (reinterpret_cast<uintptr_t>(out) & 15) == 0;
-  if (k % C::BK == 0) {
-    auto kernel = pp_gemm_kernel<true>;
+  auto launch = [&](auto kernel) {
     static std::atomic<bool> configured{false};
     if (const hipError_t e = raise_lds_limit_once(kernel, C::kLdsBytes, configured); e != hipSuccess)
       return e;
     kernel<<<grid, C::kThreads, C::kLdsBytes, stream>>>(
-        a, w, sa, static_cast<const uint16_t*>(sw), static_cast<uint16_t*>(out), m, n, k, out16);
-  } else {
-    auto kernel = pp_gemm_kernel<false>;
-    static std::atomic<bool> configured{false};
-    if (const hipError_t e = raise_lds_limit_once(kernel, C::kLdsBytes, configured); e != hipSuccess)
-      return e;
-    kernel<<<grid, C::kThreads, C::kLdsBytes, stream>>>(
-        a, w, sa, static_cast<const uint16_t*>(sw), static_cast<uint16_t*>(out), m, n, k, out16);
-  }
-  return hipGetLastError();
+        a, static_cast<const int8_t*>(w), sa, static_cast<const uint16_t*>(sw),
+        static_cast<uint16_t*>(out), m, n, k, out16);
+    return hipGetLastError();
+  };
+  const bool exact = k % C::BK == 0;
+  if (code == WeightCode::kSigned)
+    return exact ? launch(pp_gemm_kernel<true, WeightCode::kSigned>)
+                 : launch(pp_gemm_kernel<false, WeightCode::kSigned>);
+  return exact ? launch(pp_gemm_kernel<true, WeightCode::kBiasedU8>)
+               : launch(pp_gemm_kernel<false, WeightCode::kBiasedU8>);
 }
 
 }  // namespace ci8

@@ -27,10 +27,10 @@ hipError_t launch_small_m_gemm(const int8_t* a, const void* w, WeightCode code, 
                                const void* sw, void* out, int32_t* workspace, int m, int n,
                                int k, int cus, hipStream_t stream);
 
-// Large-M signed GEMM with two waves per SIMD (gemm_pp.hip); identical bits. Requires
-// a and w 16-byte aligned, sw 8-byte aligned, n % 4 == 0.
-hipError_t launch_pp_gemm(const int8_t* a, const int8_t* w, const float* sa, const void* sw,
-                          void* out, int m, int n, int k, hipStream_t stream);
+// Large-M GEMM with two waves per SIMD (gemm_pp.hip), signed or biased UINT8 weights;
+// identical bits. Requires a and w 16-byte aligned, sw 8-byte aligned, n % 4 == 0.
+hipError_t launch_pp_gemm(const int8_t* a, const void* w, WeightCode code, const float* sa,
+                          const void* sw, void* out, int m, int n, int k, hipStream_t stream);
 
 // The current device's CU count, queried once per device and cached (0 if unknown).
 int device_cu_count();

@@ -58,10 +58,11 @@ def test_gemm_schedules_match_integer_products_and_capture(ops, m, fused, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 5120, 5120), (4, 2560, 3072), (17, 37, 128),
-                                   # M >= 1024: the large-tile kernel, which debiases each
-                                   # K stage in LDS; one stage, ragged K, partial tiles
+                                   # M >= 1024: the persistent 224-wide kernel (n % 4 == 0),
+                                   # which debiases W fragments in registers, or the
+                                   # large-tile kernel; one stage, ragged K, partial tiles
                                    (1024, 224, 128), (1041, 232, 544), (2057, 480, 4096),
-                                   (1100, 17, 96), (3000, 452, 1440)])
+                                   (1100, 17, 96), (3000, 452, 1440), (5000, 2244, 2176)])
 def test_channel_mm_matches_integer_product_with_output_tails(ops, m, n, k):
     rng = np.random.default_rng(17)
     a_np, w_np, sa_np, sw_np = gemm_inputs(rng, m, n, k, biased=True)
@@ -218,7 +219,8 @@ def test_down_projection_biased_weights_full_size(ops):
 @pytest.mark.parametrize("biased", [False, True])
 def test_wide_tiles_where_they_fill_the_rounds(ops, biased):
     """M = N = 4096: 304 tiles of 256 x 224 need 2 rounds on 256 CUs and 256 tiles of
-    256 x 256 need 1, so schedule 0 (and channel_mm) runs the 256-wide kernel, with a
+    256 x 256 need 1, so schedule 0 (and channel_mm) runs the 256-wide kernel rather than
+    the persistent 224-wide one, with a
     K that is not a whole number of 128-byte stages. It agrees bit for bit with the
     128 x 128 tiling (schedule 1) and, through the exact INT32 accumulators of the
     workspace variant, with the oracle on sampled rows and columns."""
