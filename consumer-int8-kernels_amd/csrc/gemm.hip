@@ -1455,6 +1455,9 @@ hipError_t launch_grouped_summed_gemm(const int8_t* a, const int8_t* w, const fl
                                       const void* sw, void* out, int groups, int m, int n,
                                       int k, hipStream_t stream) {
   if (m <= 32) return run_grouped<Small>(a, w, sa, sw, out, groups, m, n, k, stream);
+  if (m >= 1024 && n % 4 == 0 && reinterpret_cast<uintptr_t>(sw) % 8 == 0 &&
+      groups <= grouped_pp_max_groups())
+    return launch_grouped_pp_gemm(a, w, sa, sw, out, groups, m, n, k, stream);
   return run_grouped<Medium>(a, w, sa, sw, out, groups, m, n, k, stream);
 }
 

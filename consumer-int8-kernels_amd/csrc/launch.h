@@ -41,6 +41,13 @@ hipError_t launch_grouped_summed_gemm(const int8_t* a, const int8_t* w, const fl
                                       const void* sw, void* out, int groups, int m, int n,
                                       int k, hipStream_t stream);
 
+// The same on the two-waves-per-SIMD scheme (gemm_grouped.hip); identical bits. Requires a
+// and w 16-byte aligned, sw 8-byte aligned, n % 4 == 0, groups <= grouped_pp_max_groups().
+int grouped_pp_max_groups();
+hipError_t launch_grouped_pp_gemm(const int8_t* a, const int8_t* w, const float* sa,
+                                  const void* sw, void* out, int groups, int m, int n, int k,
+                                  hipStream_t stream);
+
 // x BF16 [m, 2k] = [gate | up] -> out BF16 [m, k] = bf16(silu(gate) * up).
 hipError_t launch_silu_mul(const void* x, void* out, int m, int k, hipStream_t stream);
 // The same activations quantized per row like launch_quantize_rows, never written out.

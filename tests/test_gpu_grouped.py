@@ -109,6 +109,36 @@ def test_grouped_config5_full_size(ops):
     assert np.array_equal(bf16_bits(out), O.grouped_summed_mm(c_np, s_np, w_np, sw_np))
 
 
+@pytest.mark.parametrize("g,m,n,k", [
+    (3, 1100, 500, 1056),   # ragged M tile, K tail (8.25 stages of 128)
+    (2, 1024, 132, 128),    # one stage per group: copies cross group boundaries at once
+    (1, 1500, 260, 640),    # one group
+    (5, 2048, 256, 256),    # two stages per group
+    (48, 1024, 128, 96),    # the most groups whose row scales fit in LDS, K < one stage
+    (49, 1024, 128, 96),    # one more: the 128 x 128 kernel
+])
+def test_grouped_large_m_two_waves_per_simd(ops, g, m, n, k):
+    """M >= 1024 (n % 4 == 0) runs the two-waves-per-SIMD kernel over the groups' K stages
+    as one stream; mixed-sign channel scales, guard sentinels and a graph replay."""
+    rng = np.random.default_rng(g * 1009 + m + n + k)
+    a_np, w_np, sa_np, sw_np = grouped_inputs(rng, g, m, n, k, signed_scales=True)
+    a, w, sa, sw = to_dev(a_np), to_dev(w_np), to_dev(sa_np), to_dev(sw_np)
+    out, buf = with_guard((m, n), torch.bfloat16, float("nan"))
+    ops.grouped_summed_mm(a, w, sa, sw, out)
+    torch.cuda.synchronize()
+    want = O.grouped_summed_mm(a_np, sa_np, w_np, sw_np)
+    assert np.array_equal(bf16_bits(out), want)
+    assert guard_intact(buf, float("nan"))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.grouped_summed_mm(a, w, sa, sw, out)
+    for replay in range(2):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bf16_bits(out), want), replay
+
+
 def test_grouped_rejections(ops):
     dev = "cuda"
     a = torch.zeros(2, 8, 64, dtype=torch.int8, device=dev)
