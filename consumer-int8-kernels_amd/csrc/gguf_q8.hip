@@ -20,6 +20,8 @@
 // through two LDS buffers: while a stage is multiplied, the next stage's x and codes
 // are already in registers; the codes are dequantized to BF16 on their way into LDS,
 // once per workgroup. Rows past M or N read as zero and are not stored.
+#include <climits>
+
 #include "ci8_device.h"
 #include "launch.h"
 
@@ -159,6 +161,173 @@ __global__ void __launch_bounds__(256) gguf_q8_packed_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Small batches (m <= 16): the balanced-span layout of the W8A16 GEMV (gemv.hip).
+//
+// Workgroup (b, g) owns channels [b * span, (b + 1) * span) of group g (span = ceil(N /
+// spans), spans chosen so that about one workgroup runs per CU), walked in blocks of 16
+// channels. Its 16 waves split K into ranges of at most kSpb 64-element blocks; wave r's
+// x fragments for its range (x[0:16, g, range] as MFMA B operands, rows past m zero) are
+// loaded once into registers. Lane (row, q) of a slot takes the 16 codes at K offset
+// 64 kb + 16 q of channel row `row` and their FP16 block scale (the 16 codes lie in one
+// 32-value block), dequantizes them exactly as the tile kernel does and feeds two
+// v_mfma_f32_16x16x32_bf16. Each slot's two loads for the next block (codes, scale) are
+// issued right after its MFMAs, so at slot s of block lb the loads issued after W(lb, s)
+// are its scale, the rest of block lb and the first s slots of block lb + 1: 2 kSpb - 1
+// in all, and vmcnt(2 kSpb - 2) means both of the slot's loads have landed (the
+// prologue issues x, then W and scale of block 0 slot by slot, which gives the same
+// counts). The 16 per-range partial sums of up to 8 blocks go to LDS and are added in
+// range order with one barrier pair per 8 blocks; the last block's loads for the block
+// after it are out of range and drained before exit.
+template <int kSpb_>
+struct GgufSpanConfig {
+  static constexpr int kS = 16;       // waves, one K range each
+  static constexpr int kSpb = kSpb_;  // 64-element K blocks per range
+  static constexpr int kBatch = 8;    // blocks per partial-sum reduction (128 KiB of LDS)
+  static constexpr int kThreads = 64 * kS;
+  static_assert(2 * kSpb - 2 <= 63, "vmcnt holds 6 bits");
+};
+
+template <int kImm>
+__device__ __forceinline__ void waitcnt() {
+  __builtin_amdgcn_s_waitcnt(kImm);
+}
+
+__device__ __forceinline__ void workgroup_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Four INT8 codes -> two packed BF16 pairs bf16_rn(code * s) (exact product, one rounding).
+__device__ __forceinline__ u32x2 dequant4(uint32_t word, float s) {
+  return u32x2{pack_bf16x2(float(int8_t(word)) * s, float(int8_t(word >> 8)) * s),
+               pack_bf16x2(float(int8_t(word >> 16)) * s, float(int8_t(word >> 24)) * s)};
+}
+
+template <class C>
+__global__ void __launch_bounds__(C::kThreads) gguf_q8_span_kernel(
+    const uint16_t* __restrict__ x, const int8_t* __restrict__ codes,
+    const uint16_t* __restrict__ scales, uint16_t* __restrict__ out, int m, int n, int k,
+    int groups, int64_t xs, int64_t xg, int span) {
+  __shared__ f32x4 partial[C::kBatch][C::kS][64];
+  const int g = blockIdx.y;
+  const int c0 = int(blockIdx.x) * span;
+  if (c0 >= n) return;  // uniform over the workgroup
+  const int c_end = min(c0 + span, n);
+  const int nlocal = (c_end - c0 + 15) / 16;
+
+  const int lane = threadIdx.x & 63;
+  const int range = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row = lane & 15, q = lane >> 4;
+  const int kblocks = k / 64;
+  const int range_len = (kblocks + C::kS - 1) / C::kS;  // <= kSpb (host-checked)
+  const int kb_first = range * range_len;
+  const int my_slots = max(0, min(kb_first + range_len, kblocks) - kb_first);
+
+  // Group g's codes [n, k] and scales [n, k / 32]; x rows of group g at stride xs.
+  const int8_t* gcodes = codes + int64_t(g) * n * k;
+  const uint16_t* gscales = scales + int64_t(g) * n * (k / 32);
+  const auto w_rsrc = make_rsrc(gcodes, uint32_t(n) * uint32_t(k));
+  const auto s_rsrc = make_rsrc(gscales, uint32_t(n) * uint32_t(k / 32) * 2u);
+  const auto x_rsrc = make_rsrc(x + int64_t(g) * xg, uint32_t((int64_t(m - 1) * xs + k) * 2));
+
+  auto slot_valid = [&](int lb, int s) __attribute__((always_inline)) {
+    return c0 + lb * 16 + row < c_end && s < my_slots;
+  };
+  auto w_offset = [&](int lb, int s) __attribute__((always_inline)) {
+    const int channel = c0 + lb * 16 + row;
+    return slot_valid(lb, s)
+               ? uint32_t(channel) * uint32_t(k) + uint32_t((kb_first + s) * 64 + q * 16)
+               : kOutOfRange;
+  };
+  auto s_offset = [&](int lb, int s) __attribute__((always_inline)) {
+    const int channel = c0 + lb * 16 + row;
+    return slot_valid(lb, s)
+               ? (uint32_t(channel) * uint32_t(k / 32) + uint32_t((kb_first + s) * 2 + q / 2)) * 2u
+               : kOutOfRange;
+  };
+
+  // x fragments: lane (row, q) holds x[row, g, kb * 64 + 16 q + 8 h + 0..7].
+  u32x4 xf[C::kSpb][2];
+#pragma unroll
+  for (int s = 0; s < C::kSpb; ++s) {
+    const bool valid = row < m && s < my_slots;
+    const uint32_t base =
+        uint32_t((int64_t(row) * xs + (kb_first + s) * 64 + q * 16) * 2);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      xf[s][h] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, valid ? base + 16u * h : kOutOfRange,
+                                                       0, 0));
+  }
+  u32x4 wv[C::kSpb];
+  uint32_t sv[C::kSpb];
+#pragma unroll
+  for (int s = 0; s < C::kSpb; ++s) {
+    wv[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(0, s), 0, 0));
+    sv[s] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, s_offset(0, s), 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // Adds the partials of local blocks [lb0, lb0 + count) in range order and stores them.
+  auto reduce = [&](int lb0, int count) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+    workgroup_barrier();
+    for (int i = threadIdx.x; i < count * 256; i += C::kThreads) {
+      const int b = i >> 8, e = i & 3, l = (i >> 2) & 63;
+      const int out_row = l & 15;
+      const int out_col = c0 + (lb0 + b) * 16 + (l >> 4) * 4 + e;
+      if (out_row < m && out_col < c_end) {
+        float sum = partial[b][0][l][e];
+#pragma unroll
+        for (int v = 1; v < C::kS; ++v) sum += partial[b][v][l][e];
+        out[(int64_t(out_row) * groups + g) * n + out_col] = uint16_t(f32_to_bf16(sum));
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+    workgroup_barrier();
+  };
+
+  for (int lb = 0; lb < nlocal; ++lb) {
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < C::kSpb; ++s) {
+      waitcnt<vmcnt_imm(2 * C::kSpb - 2)>();  // W(lb, s) and its scale have landed
+      if (s < my_slots) {
+        const float sc = f16_to_f32(sv[s]);
+        const u32x4 wq = wv[s];
+        const u32x2 d0 = dequant4(wq[0], sc), d1 = dequant4(wq[1], sc);
+        const u32x2 d2 = dequant4(wq[2], sc), d3 = dequant4(wq[3], sc);
+        acc = mfma_bf16(u32x4{d0[0], d0[1], d1[0], d1[1]}, xf[s][0], acc);
+        acc = mfma_bf16(u32x4{d2[0], d2[1], d3[0], d3[1]}, xf[s][1], acc);
+      }
+      wv[s] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(lb + 1, s), 0, 0));
+      sv[s] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, s_offset(lb + 1, s), 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    partial[lb % C::kBatch][range][lane] = acc;
+    if (lb % C::kBatch == C::kBatch - 1 || lb + 1 == nlocal)  // uniform
+      reduce(lb / C::kBatch * C::kBatch, lb % C::kBatch + 1);
+  }
+  waitcnt<vmcnt_imm(0)>();  // drain the trailing (out-of-range) loads before exit
+}
+
+template <class C>
+hipError_t run_span(const void* x, const int8_t* codes, const void* scales, void* out, int m,
+                    int n, int k, int groups, int64_t xs, int64_t xg, int cus,
+                    hipStream_t stream) {
+  // About one workgroup per CU over all groups, each over at least 16 channels.
+  const int per_group = max(1, min((cus + groups - 1) / groups, (n + 15) / 16));
+  const int span = (n + per_group - 1) / per_group;
+  const dim3 grid(unsigned((n + span - 1) / span), unsigned(groups));
+  gguf_q8_span_kernel<C><<<grid, C::kThreads, 0, stream>>>(
+      static_cast<const uint16_t*>(x), codes, static_cast<const uint16_t*>(scales),
+      static_cast<uint16_t*>(out), m, n, k, groups, xs, xg, span);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_gguf_q8_packed_mm(const void* x, const int8_t* codes, const void* scales,
@@ -169,6 +338,20 @@ hipError_t launch_gguf_q8_packed_mm(const void* x, const int8_t* codes, const vo
   const auto* sp = static_cast<const uint16_t*>(scales);
   auto* op = static_cast<uint16_t*>(out);
   const unsigned tiles_n = unsigned((n + kBN - 1) / kBN);
+  // m <= 16: the balanced-span kernel while each wave's K range holds its x fragments
+  // in registers (K <= 16 ranges x 8 blocks x 64) and x's byte range fits a buffer.
+  const int cus = device_cu_count();
+  const int range_len = (k / 64 + 15) / 16;
+  if (m <= 16 && cus > 0 && range_len <= 8 && (int64_t(m - 1) * xs + k) * 2 <= INT32_MAX &&
+      int64_t(n) * k <= INT32_MAX) {
+    if (range_len <= 2)
+      return run_span<GgufSpanConfig<2>>(x, codes, scales, out, m, n, k, groups, xs, xg, cus, stream);
+    if (range_len <= 4)
+      return run_span<GgufSpanConfig<4>>(x, codes, scales, out, m, n, k, groups, xs, xg, cus, stream);
+    if (range_len <= 5)
+      return run_span<GgufSpanConfig<5>>(x, codes, scales, out, m, n, k, groups, xs, xg, cus, stream);
+    return run_span<GgufSpanConfig<8>>(x, codes, scales, out, m, n, k, groups, xs, xg, cus, stream);
+  }
   if (m <= 16) {
     gguf_q8_packed_kernel<16><<<dim3(tiles_n, unsigned(m + 15) / 16, unsigned(groups)), 256, 0,
                                 stream>>>(xp, codes, sp, op, m, n, k, groups, xs, xg);

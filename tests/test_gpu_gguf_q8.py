@@ -10,8 +10,8 @@ On top of that every output element is held to the oracle (oracle.gguf_q8_packed
 a float64 product of the same BF16 weights): |out - exact| <= one BF16 ulp of the exact
 value + K * 2^-24 * sum_k |x * wq| (any FP32 summation order). Further cases reach
 ragged N (scalar stores), padded row strides, a single K stage, large K, M on both
-sides of the 16-row tile switch, extreme codes and scales, and guard sentinels around
-the output.
+sides of the 16-row switch (m <= 16 runs the balanced-span kernel of the W8A16 GEMV
+while K <= 8192), extreme codes and scales, and guard sentinels around the output.
 """
 
 import numpy as np
@@ -92,8 +92,11 @@ CASES = [
     (17, 1, 1000, 5120, 0),     # smallest M of the 64-row tile, ragged N
     (200, 2, 130, 1536, 64),    # ragged M and N (N % 4 == 2: scalar stores), padded rows
     (64, 4, 96, 64, 8),         # one K stage
-    (5, 2, 37, 16384, 0),       # long K
+    (5, 2, 37, 16384, 0),       # long K: the tile kernel at m <= 16
     (256, 1, 512, 2048, 0),
+    (7, 3, 300, 2048, 64),      # m <= 16 span kernel: groups, padded rows, ragged spans
+    (16, 2, 4100, 8192, 0),     # span kernel at its longest K, more channels than CUs x 16
+    (2, 5, 16, 64, 8),          # one channel block per group, one K block
 ]
 
 
