@@ -29,6 +29,7 @@ SIGNATURES = {
     "ci8_quantize_grouped4096": ([_p, _p, _p, _i64, _i64, _p], ctypes.c_int),
     "ci8_fused_channel_mm": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p], ctypes.c_int),
     "ci8_cutlass_channel_mm": ([_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p], ctypes.c_int),
+    "ci8_cutlass_channel_mm_noalloc": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p], ctypes.c_int),
     "ci8_channel_mm": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p], ctypes.c_int),
     "ci8_channel_gemv": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], ctypes.c_int),
     "ci8_grouped_summed_mm": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p], ctypes.c_int),

@@ -124,6 +124,21 @@ int ci8_cutlass_channel_mm(const int8_t* a, const int8_t* w, const float* a_scal
                                            as_stream(stream)));
 }
 
+int ci8_cutlass_channel_mm_noalloc(const int8_t* a, const int8_t* w, const float* a_scale,
+                                   const void* w_scale, void* out, int64_t m, int64_t n,
+                                   int64_t k, void* stream) {
+  if (int s = check_gemm(m, n, k, true, "Invalid CUTLASS geometry")) return s;
+  if (m * n > ci8::noalloc_scratch_ints())
+    return fail(CI8_ERR_TOO_LARGE,
+                "cutlass_channel_mm_noalloc: m * n exceeds the library's scratch of "
+                "8388608 INT32 accumulators; use cutlass_channel_mm with a workspace");
+  if (!aligned(a, 16) || !aligned(w, 16) || !aligned(a_scale, 4) || !aligned(w_scale, 2) ||
+      !aligned(out, 2))
+    return fail(CI8_ERR_ALIGNMENT, "cutlass_channel_mm requires aligned buffers");
+  return launched(ci8::launch_cutlass_channel_mm_noalloc(a, w, a_scale, w_scale, out, int(m),
+                                                         int(n), int(k), as_stream(stream)));
+}
+
 int ci8_channel_mm(const int8_t* a, const uint8_t* w_u8, const float* a_scale,
                    const void* w_scale, void* out, int64_t m, int64_t n, int64_t k,
                    void* stream) {

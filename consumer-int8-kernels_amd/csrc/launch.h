@@ -21,6 +21,14 @@ hipError_t launch_channel_gemm(const int8_t* a, const void* w, WeightCode code,
                                int32_t* workspace, int m, int n, int k, int schedule,
                                hipStream_t stream);
 
+// launch_channel_gemm for signed weights with the INT32 accumulators written to the
+// library's own device array instead of a caller workspace (noalloc.hip). Requires
+// m * n <= noalloc_scratch_ints(); allocates nothing.
+int64_t noalloc_scratch_ints();
+hipError_t launch_cutlass_channel_mm_noalloc(const int8_t* a, const int8_t* w, const float* sa,
+                                             const void* sw, void* out, int m, int n, int k,
+                                             hipStream_t stream);
+
 // Small-M variant of launch_channel_gemm (gemm_small.hip): small output tiles, K split
 // over the workgroup's waves; identical bits. `cus` is the device's CU count.
 hipError_t launch_small_m_gemm(const int8_t* a, const void* w, WeightCode code, const float* sa,

@@ -3,7 +3,8 @@
  * Every entry point takes raw device pointers, int64 sizes and a HIP stream passed as
  * `void*` (a hipStream_t; NULL selects the null stream). Calls are asynchronous and
  * stream-ordered, allocate nothing, keep no mutable global state and write only the
- * caller-owned outputs, so they can be captured into a HIP graph.
+ * caller-owned outputs (ci8_cutlass_channel_mm_noalloc also writes the library's own
+ * device scratch array), so they can be captured into a HIP graph.
  *
  * Each function validates its arguments before touching the GPU. A rejected call
  * returns a CI8_ERR_* code without launching anything; the message is available from
@@ -15,6 +16,8 @@
  *   ci8_quantize_grouped4096 csrc/kernels.h:50-51, csrc/bindings.cpp:210-237, schema :604
  *   ci8_fused_channel_mm     csrc/kernels.h:27-28, csrc/bindings.cpp:386-427, schema :598
  *   ci8_cutlass_channel_mm   csrc/kernels.h:63-65, csrc/bindings.cpp:386-424, schema :610
+ *   ci8_cutlass_channel_mm_noalloc  no reference counterpart (cutlass_channel_mm without
+ *                            the caller's workspace, for callers that cannot allocate)
  *   ci8_channel_mm           csrc/kernels.h:56-58, csrc/bindings.cpp:238-265, schema :605
  *   ci8_grouped_summed_mm    no reference op (configs[4]'s summed grouped W8A8); the
  *                            closest reference code is benchmarks/cuda/q8_block_int8.cu:54-55
@@ -94,6 +97,20 @@ int ci8_fused_channel_mm(const int8_t* a, const int8_t* w, const float* a_scale,
 int ci8_cutlass_channel_mm(const int8_t* a, const int8_t* w, const float* a_scale,
                            const void* w_scale, int32_t* workspace, void* out, int64_t m,
                            int64_t n, int64_t k, void* stream);
+
+/* cutlass_channel_mm_noalloc: cutlass_channel_mm with no workspace argument; the INT32
+ * accumulators go to a device array the library holds on each GPU it runs on (32 MiB,
+ * kept until the process ends). out is bit-identical to cutlass_channel_mm's. Allocates
+ * nothing: no hipMalloc, no allocating library call. Requires what cutlass_channel_mm
+ * requires, and m * n <= 8388608 (else CI8_ERR_TOO_LARGE). Calls that overlap in time on
+ * one GPU share the array and race on it (their outputs are unaffected: nothing reads
+ * the array back).
+ * No counterpart in the reference: it is for callers that cannot allocate the workspace
+ * tensor cutlass_channel_mm needs (code under HIP graph capture, serving loops that
+ * forbid allocation). */
+int ci8_cutlass_channel_mm_noalloc(const int8_t* a, const int8_t* w, const float* a_scale,
+                                   const void* w_scale, void* out, int64_t m, int64_t n,
+                                   int64_t k, void* stream);
 
 /* channel_mm: as fused_channel_mm with biased UINT8 weights w_u8 [n,k] holding
  * signed code + 128 (the weight used is w_u8 - 128). Any n > 0.

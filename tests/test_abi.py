@@ -20,7 +20,8 @@ def declared_functions():
 def test_header_declares_the_expected_entry_points():
     assert declared_functions() == sorted([
         "ci8_last_error", "ci8_version", "ci8_quantize_rows", "ci8_quantize_grouped4096",
-        "ci8_fused_channel_mm", "ci8_cutlass_channel_mm", "ci8_channel_mm",
+        "ci8_fused_channel_mm", "ci8_cutlass_channel_mm", "ci8_cutlass_channel_mm_noalloc",
+        "ci8_channel_mm",
         "ci8_channel_gemv", "ci8_grouped_summed_mm", "ci8_silu_mul", "ci8_silu_mul_quantize",
         "ci8_unpack_allspark", "ci8_quantize_block32", "ci8_q8_block_mm", "ci8_q8_block_int8",
         "ci8_gguf_q8_packed_mm",
@@ -87,6 +88,25 @@ def test_fused_and_cutlass_geometry_rejections(lib, m, n, k):
            A.CI8_ERR_GEOMETRY, "Invalid CUTLASS geometry")
     expect(lib, lib.ci8_cutlass_channel_mm(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, m, n, k, None),
            A.CI8_ERR_GEOMETRY, "Invalid CUTLASS geometry")
+    expect(lib, lib.ci8_cutlass_channel_mm_noalloc(FAKE, FAKE, FAKE, FAKE, FAKE, m, n, k, None),
+           A.CI8_ERR_GEOMETRY, "Invalid CUTLASS geometry")
+
+
+def test_noalloc_scratch_limit_and_alignment(lib):
+    """The no-allocation variant refuses m * n beyond its 8,388,608-entry scratch (the
+    limit itself is accepted up to the alignment check) and checks alignment like
+    cutlass_channel_mm."""
+    from consumer_int8 import _abi as A
+
+    f = lib.ci8_cutlass_channel_mm_noalloc
+    expect(lib, f(FAKE, FAKE, FAKE, FAKE, FAKE, 2048, 4100, 32, None), A.CI8_ERR_TOO_LARGE,
+           "exceeds the library's scratch of 8388608 INT32 accumulators")
+    expect(lib, f(FAKE, FAKE, FAKE, FAKE, FAKE, 8192, 1028, 32, None), A.CI8_ERR_TOO_LARGE,
+           "exceeds the library's scratch")
+    expect(lib, f(FAKE + 8, FAKE, FAKE, FAKE, FAKE, 2048, 4096, 32, None), A.CI8_ERR_ALIGNMENT,
+           "cutlass_channel_mm requires aligned buffers")
+    expect(lib, f(FAKE, FAKE, FAKE, FAKE, FAKE + 1, 4, 4, 32, None), A.CI8_ERR_ALIGNMENT,
+           "aligned")
 
 
 def test_fused_schedule_alignment_and_size_rejections(lib):
