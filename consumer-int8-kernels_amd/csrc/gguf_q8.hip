@@ -13,14 +13,19 @@
 // Layout: x BF16 [M, G, K] with independent row and group strides (K contiguous), codes
 // INT8 [G, N, K], scales FP16 [G, N, K / 32], out BF16 [M, G, N] contiguous; K % 64 == 0.
 //
-// Design: a workgroup computes a BM x 64 (rows x channels) tile of one group; its four
-// waves each own a 16-channel block and BM / 16 row blocks of
-// v_mfma_f32_16x16x32_bf16 accumulators (the MFMA computes D[n][m] = Wq . x^T, so a lane
-// holds 4 consecutive channels of one row and stores 8 bytes). K advances 64 at a time
-// through two LDS buffers: while a stage is multiplied, the next stage's x and codes
-// are already in registers; the codes are dequantized to BF16 on their way into LDS,
-// once per workgroup. Rows past M or N read as zero and are not stored.
+// Kernels, all on v_mfma_f32_16x16x32_bf16 with the MFMA computing D[n][m] = Wq . x^T
+// (a lane holds 4 consecutive channels of one row and stores 8 bytes):
+//  * m <= 16, K <= 8192: the balanced-span kernel (the layout of the W8A16 GEMV).
+//  * m > 16: 256 x 128 or 128 x 128 tiles of eight waves with an LDS ring of three K
+//    stages, codes dequantized once per tile and stage (gguf_q8_large_kernel).
+//  * Otherwise (x or the codes beyond a 2 GiB buffer range, or m <= 16 with K > 8192):
+//    a BM x 64 tile of four waves, each owning a 16-channel block and BM / 16 row blocks;
+//    K advances 64 at a time through two LDS buffers while the next stage's x and codes
+//    wait in registers, and the codes are dequantized on their way into LDS.
+// Rows past M or N read as zero and are not stored.
+#include <atomic>
 #include <climits>
+#include <type_traits>
 
 #include "ci8_device.h"
 #include "launch.h"
@@ -328,6 +333,246 @@ hipError_t run_span(const void* x, const int8_t* codes, const void* scales, void
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------
+// Large batches: a BM x 128 (rows x channels) tile per workgroup of eight waves.
+//
+// The BM x 64 tile kernel above dequantizes each weight stage once per 64 rows and runs
+// 8 MFMAs a wave per stage between barriers, which leaves it bound by dequantization and
+// synchronisation. Here a tile is 256 (or 128) rows by 128 channels: wave w owns 64 rows
+// (w % WM) and 128 / WN channels (w / WM) as 4 x TN accumulator blocks, 32 (or 16)
+// MFMAs a wave per 64-wide K stage, and each stage's codes are dequantized once for 256
+// (128) rows.
+//  * LDS holds a ring of three stages, each x [BM][64] BF16 then Wq [128][64] BF16,
+//    rows of 128 bytes with 16-byte chunks XOR-swizzled by row % 8.
+//  * x goes global -> LDS by buffer_load ... lds (8 rows x 128 bytes a copy; rows past
+//    M are out of the buffer's range and arrive as zeros). Each thread loads the 16
+//    codes of one channel at one 16-value K offset and their FP16 block scale into
+//    registers, two stages ahead, and dequantizes them into the ring one stage ahead.
+//  * Stage t: issue stage t + 2's copies and code loads, read stage t's fragments, run
+//    the K-step-0 MFMAs, wait for stage t + 1's loads (vmcnt counts the newer copies and
+//    loads), dequantize stage t + 1's codes into its slot while the K-step-1 MFMAs run,
+//    then one barrier. A slot is refilled two stages after it was read, past a barrier.
+// One 16-byte-per-lane LDS DMA copy (a non-template helper: the host pass of a kernel
+// template rejects the 16-byte form of the builtin, which only gfx950 has).
+__device__ __forceinline__ void copy16_lds(__amdgpu_buffer_rsrc_t rsrc, lds_void* dst,
+                                           uint32_t offset, int soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, offset, soffset, 0, 0);
+}
+
+template <int BM_>
+struct GgufLargeConfig {
+  static constexpr int BM = BM_, BN = 128, kWaves = 8, kThreads = 64 * kWaves;
+  static constexpr int WM = BM / 64;            // waves along rows (64 rows each)
+  static constexpr int WN = kWaves / WM;        // waves along channels
+  static constexpr int TM = 4;                  // 16-row blocks per wave
+  static constexpr int TN = BN / WN / 16;       // 16-channel blocks per wave
+  static constexpr int kXBytes = BM * 128;      // one stage of x: BM rows x 64 BF16
+  static constexpr int kWBytes = BN * 128;      // one stage of Wq: 128 channels x 64 BF16
+  static constexpr int kStageBytes = kXBytes + kWBytes;
+  static constexpr int kLdsBytes = 3 * kStageBytes;
+  static constexpr int kXCopies = kXBytes / 1024 / kWaves;  // 1 KiB copies per wave per stage
+  static constexpr int GROUP_M = 8;
+  static_assert(WM * WN == kWaves && TN >= 1, "wave grid");
+  static_assert(kXCopies * kWaves * 1024 == kXBytes, "x copies");
+  static_assert(BN * 4 == kThreads, "one thread per 16 codes of a stage");
+  static_assert(kLdsBytes <= 160 * 1024, "LDS");
+  static_assert(kXCopies + 2 <= 63, "vmcnt");
+};
+
+template <class C>
+__global__ void __launch_bounds__(C::kThreads, 1) gguf_q8_large_kernel(
+    const uint16_t* __restrict__ x, const int8_t* __restrict__ codes,
+    const uint16_t* __restrict__ scales, uint16_t* __restrict__ out, int m, int n, int k,
+    int groups, int64_t xs, int64_t xg, int tiles_m, int tiles_n) {
+  extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
+  auto* lds = (char __attribute__((address_space(3)))*)(lds_raw);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // Workgroup -> (group, tile). The hardware deals workgroups round-robin over the 8
+  // XCDs; undo that so each XCD runs a contiguous range of logical tiles, ordered as a
+  // raster of GROUP_M row tiles so that tiles sharing a weight panel run together.
+  const int tiles = tiles_m * tiles_n;
+  const int total = tiles * groups;
+  int logical = int(blockIdx.x);
+  {
+    constexpr int kXcds = 8;
+    const int per = total / kXcds, extra = total % kXcds;
+    const int xcd = logical % kXcds, idx = logical / kXcds;
+    logical = (xcd < extra ? xcd * (per + 1) : extra * (per + 1) + (xcd - extra) * per) + idx;
+  }
+  const int g = logical / tiles;
+  const int tile = logical - g * tiles;
+  const int group_span = C::GROUP_M * tiles_n;
+  const int first_m = (tile / group_span) * C::GROUP_M;
+  const int group_rows = min(tiles_m - first_m, C::GROUP_M);
+  const int m0 = (first_m + (tile % group_span) % group_rows) * C::BM;
+  const int n0 = ((tile % group_span) / group_rows) * C::BN;
+
+  const auto x_rsrc = make_rsrc(x + int64_t(g) * xg, uint32_t((int64_t(m - 1) * xs + k) * 2));
+  const auto c_rsrc = make_rsrc(codes + int64_t(g) * n * k, uint32_t(n) * uint32_t(k));
+  const auto s_rsrc = make_rsrc(scales + int64_t(g) * n * (k / 32), uint32_t(n) * uint32_t(k / 32) * 2u);
+
+  // x copy q of this wave brings rows 8 b .. 8 b + 7 (b = wave * kXCopies + q): lane ->
+  // row 8 b + lane / 8, LDS chunk slot lane % 8 holding logical chunk slot ^ (row % 8).
+  uint32_t x_off[C::kXCopies];
+#pragma unroll
+  for (int q = 0; q < C::kXCopies; ++q) {
+    const int row = (wave * C::kXCopies + q) * 8 + (lane >> 3);
+    const int chunk = (lane & 7) ^ (lane >> 3);
+    x_off[q] = m0 + row < m ? uint32_t(int64_t(m0 + row) * xs * 2) + uint32_t(chunk * 16)
+                            : kOutOfRange;
+  }
+  // Codes: thread -> channel c_row of the tile, 16 codes at K offset c_col of a stage.
+  const int c_row = tid >> 2, c_col = (tid & 3) * 16;
+  const bool c_live = n0 + c_row < n;
+  const uint32_t c_off = c_live ? uint32_t(n0 + c_row) * uint32_t(k) + uint32_t(c_col) : kOutOfRange;
+  const uint32_t s_off =
+      c_live ? (uint32_t(n0 + c_row) * uint32_t(k / 32) + uint32_t(c_col / 32)) * 2u : kOutOfRange;
+
+  const int ns = k / 64;
+  // Stage t's copies and code loads. Stages past the end issue the same instructions
+  // with out-of-range offsets (no memory traffic; the zeros land in a slot no stage
+  // reads again), so every path has the same number of loads in flight and each wait
+  // below is one constant count.
+  auto issue = [&] __device__(int t, u32x4& cr, uint32_t& sr) __attribute__((always_inline)) {
+    const bool live = t < ns;  // uniform
+    auto* slot = lds + (t % 3) * C::kStageBytes;
+#pragma unroll
+    for (int q = 0; q < C::kXCopies; ++q)
+      copy16_lds(x_rsrc, reinterpret_cast<lds_void*>(slot + (wave * C::kXCopies + q) * 1024),
+                 live ? x_off[q] : kOutOfRange, t * 128);
+    cr = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(c_rsrc, live ? c_off : kOutOfRange, t * 64, 0));
+    sr = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, live ? s_off : kOutOfRange, t * 4, 0);
+  };
+  // Dequantized codes of stage t -> its slot's Wq rows (2 chunks of 8 BF16).
+  auto dequant = [&] __device__(int t, const u32x4& cr, uint32_t sr) __attribute__((always_inline)) {
+    auto* wbase = lds + (t % 3) * C::kStageBytes + C::kXBytes;
+    const float s = f16_to_f32(sr);
+    uint32_t packed[8];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t word = cr[w];
+      packed[2 * w] = pack_bf16x2(float(int8_t(word)) * s, float(int8_t(word >> 8)) * s);
+      packed[2 * w + 1] = pack_bf16x2(float(int8_t(word >> 16)) * s, float(int8_t(word >> 24)) * s);
+    }
+    const int chunk = c_col / 8;
+    *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(wbase + tile_offset(c_row, chunk)) =
+        u32x4{packed[0], packed[1], packed[2], packed[3]};
+    *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(wbase + tile_offset(c_row, chunk + 1)) =
+        u32x4{packed[4], packed[5], packed[6], packed[7]};
+  };
+
+  // Fragments: row lane % 16 of a 16-row block, K elements 8 (lane / 16) .. + 7 of K-step
+  // h, i.e. 16-byte chunk 4 h + lane / 16 of the stage.
+  const int f_row = lane & 15, f_chunk = lane >> 4;
+  const int wm = wave % C::WM, wn = wave / C::WM;
+  f32x4 acc[C::TM][C::TN];
+#pragma unroll
+  for (int j = 0; j < C::TM; ++j)
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 cr[2];
+  uint32_t sr[2];
+  issue(0, cr[0], sr[0]);
+  issue(1, cr[1], sr[1]);
+  waitcnt<vmcnt_imm(C::kXCopies + 2)>();  // stage 0's copies and codes landed
+  dequant(0, cr[0], sr[0]);
+  __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+  workgroup_barrier();
+
+  // Stage t's fragments and MFMAs, K-step h.
+  u32x4 xf[2][C::TM], wf[2][C::TN];
+  auto read_stage = [&] __device__(int t) __attribute__((always_inline)) {
+    const auto* slot = lds + (t % 3) * C::kStageBytes;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int i = 0; i < C::TN; ++i)
+        wf[h][i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+            slot + C::kXBytes + tile_offset(wn * (C::TN * 16) + i * 16 + f_row, 4 * h + f_chunk));
+#pragma unroll
+      for (int j = 0; j < C::TM; ++j)
+        xf[h][j] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+            slot + tile_offset(wm * 64 + j * 16 + f_row, 4 * h + f_chunk));
+    }
+  };
+  auto mfmas = [&] __device__(int h) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i)
+#pragma unroll
+      for (int j = 0; j < C::TM; ++j) acc[j][i] = mfma_bf16(wf[h][i], xf[h][j], acc[j][i]);
+  };
+  // A stage with a successor; register set R = t % 2 holds the codes of stages t and
+  // t + 2. The body is the same for every such stage (no data-dependent branch), so the
+  // compiler's own waits see one load pattern.
+  auto step = [&] __device__(int t, u32x4& cr_next2, uint32_t& sr_next2, const u32x4& cr_next,
+                  uint32_t sr_next) __attribute__((always_inline)) {
+    issue(t + 2, cr_next2, sr_next2);
+    read_stage(t);
+    mfmas(0);
+    // Keep the dequantization behind the first MFMAs (the scheduler would otherwise
+    // hoist it, and the wait for its codes, to the top of the stage).
+    __builtin_amdgcn_sched_barrier(0);
+    waitcnt<vmcnt_imm(C::kXCopies + 2)>();  // stage t + 1's copies and codes landed
+    dequant(t + 1, cr_next, sr_next);
+    mfmas(1);
+    __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+    workgroup_barrier();
+  };
+  int t = 0;
+  for (; t + 2 < ns; t += 2) {
+    step(t, cr[0], sr[0], cr[1], sr[1]);
+    step(t + 1, cr[1], sr[1], cr[0], sr[0]);
+  }
+  if (t + 1 < ns) {  // two stages left
+    step(t, cr[0], sr[0], cr[1], sr[1]);
+    ++t;
+  }
+  read_stage(t);  // the last stage
+  mfmas(0);
+  mfmas(1);
+  waitcnt<vmcnt_imm(0)>();  // drain the trailing (out-of-range) copies before exit
+
+  // Lane holds D[n][m] for channels 4 (lane / 16) .. + 3 of each channel block and row
+  // lane % 16 of each row block.
+  const bool vec = (n & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 7) == 0;
+#pragma unroll
+  for (int j = 0; j < C::TM; ++j) {
+    const int row = m0 + wm * 64 + j * 16 + f_row;
+    if (row >= m) continue;
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i) {
+      const int col = n0 + wn * (C::TN * 16) + i * 16 + 4 * f_chunk;
+      uint16_t* dst = out + (int64_t(row) * groups + g) * n + col;
+      if (vec && col + 3 < n) {
+        *reinterpret_cast<u32x2*>(dst) =
+            u32x2{pack_bf16x2(acc[j][i][0], acc[j][i][1]), pack_bf16x2(acc[j][i][2], acc[j][i][3])};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (col + e < n) dst[e] = uint16_t(f32_to_bf16(acc[j][i][e]));
+      }
+    }
+  }
+}
+
+template <class C>
+hipError_t run_large(const void* x, const int8_t* codes, const void* scales, void* out, int m,
+                     int n, int k, int groups, int64_t xs, int64_t xg, hipStream_t stream) {
+  static std::atomic<bool> configured{false};
+  if (const hipError_t e = raise_lds_limit_once(gguf_q8_large_kernel<C>, C::kLdsBytes, configured);
+      e != hipSuccess)
+    return e;
+  const int tiles_m = (m + C::BM - 1) / C::BM, tiles_n = (n + C::BN - 1) / C::BN;
+  gguf_q8_large_kernel<C><<<unsigned(tiles_m * tiles_n * groups), C::kThreads, C::kLdsBytes, stream>>>(
+      static_cast<const uint16_t*>(x), codes, static_cast<const uint16_t*>(scales),
+      static_cast<uint16_t*>(out), m, n, k, groups, xs, xg, tiles_m, tiles_n);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_gguf_q8_packed_mm(const void* x, const int8_t* codes, const void* scales,
@@ -351,6 +596,20 @@ hipError_t launch_gguf_q8_packed_mm(const void* x, const int8_t* codes, const vo
     if (range_len <= 5)
       return run_span<GgufSpanConfig<5>>(x, codes, scales, out, m, n, k, groups, xs, xg, cus, stream);
     return run_span<GgufSpanConfig<8>>(x, codes, scales, out, m, n, k, groups, xs, xg, cus, stream);
+  }
+  // m > 16: 128-channel tiles of 256 or 128 rows (while x's and the codes' byte ranges
+  // fit a buffer's), whichever takes fewer rounds of one tile per CU, a round of 256-row
+  // tiles costing about 1.45 rounds of 128-row ones (measured on MI355X at K = 2048 ..
+  // 5120; either beats the 64 x 64 tiles at every M from 64 up).
+  const int64_t tiles_n128 = (n + 127) / 128;
+  const int64_t tiles256 = (m + 255) / 256 * tiles_n128 * groups;
+  const int64_t tiles128 = (m + 127) / 128 * tiles_n128 * groups;
+  if (m > 16 && cus > 0 && (int64_t(m - 1) * xs + k) * 2 <= INT32_MAX &&
+      int64_t(n) * k <= INT32_MAX && tiles128 <= INT32_MAX) {
+    const int64_t rounds256 = (tiles256 + cus - 1) / cus, rounds128 = (tiles128 + cus - 1) / cus;
+    if (rounds256 * 29 <= rounds128 * 20)
+      return run_large<GgufLargeConfig<256>>(x, codes, scales, out, m, n, k, groups, xs, xg, stream);
+    return run_large<GgufLargeConfig<128>>(x, codes, scales, out, m, n, k, groups, xs, xg, stream);
   }
   if (m <= 16) {
     gguf_q8_packed_kernel<16><<<dim3(tiles_n, unsigned(m + 15) / 16, unsigned(groups)), 256, 0,

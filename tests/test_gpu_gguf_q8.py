@@ -11,7 +11,9 @@ a float64 product of the same BF16 weights): |out - exact| <= one BF16 ulp of th
 value + K * 2^-24 * sum_k |x * wq| (any FP32 summation order). Further cases reach
 ragged N (scalar stores), padded row strides, a single K stage, large K, M on both
 sides of the 16-row switch (m <= 16 runs the balanced-span kernel of the W8A16 GEMV
-while K <= 8192), extreme codes and scales, and guard sentinels around the output.
+while K <= 8192), the 256- and 128-row tiles of larger batches (1, 2, 3, 7 and 8 K
+stages), the 64-row tile kernel that takes x beyond a 2 GiB buffer range, extreme codes
+and scales, and guard sentinels around the output.
 """
 
 import numpy as np
@@ -89,7 +91,7 @@ def test_reference_cases_with_graph_replay(gguf, m, group_major):
 CASES = [
     # m, groups, n, k, row padding (elements beyond G*K per row)
     (16, 1, 4096, 4096, 0),     # largest M of the 16-row tile
-    (17, 1, 1000, 5120, 0),     # smallest M of the 64-row tile, ragged N
+    (17, 1, 1000, 5120, 0),     # smallest M past the span kernel, ragged N
     (200, 2, 130, 1536, 64),    # ragged M and N (N % 4 == 2: scalar stores), padded rows
     (64, 4, 96, 64, 8),         # one K stage
     (5, 2, 37, 16384, 0),       # long K: the tile kernel at m <= 16
@@ -97,6 +99,12 @@ CASES = [
     (7, 3, 300, 2048, 64),      # m <= 16 span kernel: groups, padded rows, ragged spans
     (16, 2, 4100, 8192, 0),     # span kernel at its longest K, more channels than CUs x 16
     (2, 5, 16, 64, 8),          # one channel block per group, one K block
+    # M > 16: 128-channel tiles of 256 or 128 rows (the smaller shapes above run 128 rows)
+    (2048, 1, 4096, 512, 0),    # 256-row tiles, even stage count
+    (1100, 2, 4002, 192, 8),    # 256-row tiles, ragged M, N % 4 == 2, three stages
+    (600, 4, 2000, 448, 24),    # 128-row tiles, ragged M and N, odd stage count
+    (2048, 1, 4096, 64, 0),     # a single K stage
+    (1024, 2, 4096, 128, 0),    # two K stages
 ]
 
 
@@ -165,3 +173,37 @@ def test_empty_outputs_and_rejections(gguf):
     bad[0, 0, 0, :2] = torch.tensor([0x00, 0x7C], dtype=torch.uint8)  # FP16 +inf
     with pytest.raises(ValueError, match="must be finite"):
         gguf.pack_q8(bad.cuda())
+
+
+def test_group_major_large_tiles(gguf):
+    """x as a group-major view (group stride < row stride is not required: here the
+    group stride is M * K and the row stride K) on the 128-row tiles."""
+    gen = torch.Generator().manual_seed(91)
+    m, groups, n, k = 512, 4, 2048, 256
+    raw, codes_cpu, scales_cpu = raw_blocks(gen, groups, n, k)
+    codes, scales = gguf.pack_q8(raw.cuda())
+    x = torch.randn(groups, m, k, generator=gen).bfloat16().cuda().transpose(0, 1)
+    assert x.stride() == (k, m * k, 1)
+    out = torch.empty(m, groups, n, device="cuda", dtype=torch.bfloat16)
+    gguf.q8_packed_mm(x, codes, scales, out)
+    torch.cuda.synchronize()
+    check(bf16_bits(out), bf16_bits(x.contiguous()), codes_cpu.numpy(),
+          scales_cpu.view(torch.int16).numpy().view(np.uint16), rel_norm=0.001)
+
+
+def test_x_beyond_buffer_range_takes_the_tile_kernel(gguf):
+    """A row stride of 2^27 elements puts x's byte range (19 rows x 256 MiB) past what a
+    buffer descriptor addresses, so M = 20 runs the 64-row tile kernel."""
+    m, groups, n, k, xs = 20, 1, 200, 256, 1 << 27
+    rng = np.random.default_rng(5)
+    x_np = O.f32_to_bf16(rng.standard_normal((m, groups, k)).astype(np.float32))
+    codes_np = rng.integers(-128, 128, (groups, n, k)).astype(np.int8)
+    scales_np = (rng.random((groups, n, k // 32)) * 0.02).astype(np.float16).view(np.uint16)
+    big = torch.zeros((m - 1) * xs + groups * k, device="cuda", dtype=torch.bfloat16)
+    x = torch.as_strided(big, (m, groups, k), (xs, k, 1))
+    x.copy_(to_dev(x_np))
+    out = torch.empty(m, groups, n, device="cuda", dtype=torch.bfloat16)
+    gguf.q8_packed_mm(x, to_dev(codes_np), to_dev(scales_np).view(torch.float16), out)
+    torch.cuda.synchronize()
+    check(bf16_bits(out), x_np, codes_np, scales_np, rel_norm=0.001)
+    del big
