@@ -17,7 +17,8 @@ GEMV, the grouped summed GEMM, the biased-UINT8 down
 projection with its SwiGLU activation producers (silu_mul_quantize,
 silu_mul), the AllSpark weight restore (unpack_allspark), the block-32 Q8_0 W8A8 GEMM,
 the GGUF Q8_0 grouped W8A16 op (gguf_q8_packed_mm) and the small quantize + GEMM pass
-(configs[0]); and
+(configs[0]); `vendor_int_mm_cfg3`, the vendor library's INT8 GEMM (torch._int_mm, i.e.
+hipBLASLt, INT32 output) on the headline shape and inputs, for reference; and
 `cpu_baseline`, the reference's torch CPU math for the same step on a bounded row slice,
 on this host's cores.
 
@@ -524,6 +525,23 @@ def main() -> int:
                     "mean_us": round(mean_us, 2), "flops": fg}
             del xg, og
         del gq, gs
+        # The vendor library on the headline shape, for reference: torch._int_mm (hipBLASLt's
+        # INT8 GEMM, INT32 output, no scale epilogue) on the same codes and weights.
+        try:
+            calls = [lambda i=i: torch._int_mm(codes[i % len(codes)], ws[i % len(ws)].t())
+                     for i in range(len(ws))]
+            for c in calls:
+                c()
+            condition(torch, calls)
+            mean_us, _ = time_kernel(torch, calls, 4)
+            tops = GEMM_OPS / (mean_us * 1e-6) / 1e12
+            extras["vendor_int_mm_cfg3"] = {
+                "bound": "mfma", "achieved": round(tops, 1), "peak": round(peak_tops, 1),
+                "unit": "TOPS", "frac": round(tops / peak_tops, 4), "mean_us": round(mean_us, 2),
+                "library": "torch._int_mm (hipBLASLt), INT32 output"}
+        except RuntimeError as error:  # an INT8 GEMM the installed torch does not offer
+            extras["vendor_int_mm_cfg3"] = {"error": str(error)[:200]}
+        torch.cuda.synchronize()
         # quantize_rows + fused_channel_mm at M=128, K=4096, N=4096; AI 234
         # op/B is below the ridge, so this small case is bounded by HBM (bytes below).
         M1, K1, N1 = 128, 4096, 4096
