@@ -31,7 +31,7 @@ HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["quantize.hip", "gemm.hip", "gemm_small.hip", "gemm_pp.hip", "gemv.hip", "silu.hip",
-               "allspark.hip", "q8block.hip", "gguf_q8.hip", "gemm_grouped.hip", "noalloc.hip"]
+               "allspark.hip", "q8block.hip", "gguf_q8.hip", "gemm_grouped.hip", "noalloc.hip", "gemm_bytes.hip"]
 HOST_SOURCES = ["abi.cpp"]
 
 # -packed-fp32-ops: keep packed FP32 (v_pk_*_f32) out of the generated code.

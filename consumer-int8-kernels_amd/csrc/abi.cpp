@@ -146,9 +146,14 @@ int ci8_channel_mm(const int8_t* a, const uint8_t* w_u8, const float* a_scale,
     return fail(CI8_ERR_GEOMETRY, "Invalid matrix geometry");
   if (m * k > INT_MAX || n * k > INT_MAX || m * n > INT_MAX)
     return fail(CI8_ERR_TOO_LARGE, "Matrix too large");
-  if (!aligned(a, 16) || !aligned(w_u8, 16) || !aligned(a_scale, 4) || !aligned(w_scale, 2) ||
-      !aligned(out, 2))
+  if (!aligned(a_scale, 4) || !aligned(w_scale, 2) || !aligned(out, 2))
     return fail(CI8_ERR_ALIGNMENT, "channel_mm requires aligned buffers");
+  // The reference accepts operands at any offset (csrc/bindings.cpp:238-265); the MFMA
+  // kernels copy 16-byte chunks, so other alignments take the byte-load kernel.
+  if (!aligned(a, 16) || !aligned(w_u8, 16))
+    return launched(ci8::launch_channel_gemm_bytes(a, w_u8, ci8::WeightCode::kBiasedU8,
+                                                   a_scale, w_scale, out, int(m), int(n),
+                                                   int(k), as_stream(stream)));
   return launched(ci8::launch_channel_gemm(a, w_u8, ci8::WeightCode::kBiasedU8, a_scale,
                                            w_scale, out, nullptr, int(m), int(n), int(k), 0,
                                            as_stream(stream)));

@@ -29,6 +29,12 @@ hipError_t launch_cutlass_channel_mm_noalloc(const int8_t* a, const int8_t* w, c
                                              const void* sw, void* out, int m, int n, int k,
                                              hipStream_t stream);
 
+// launch_channel_gemm (schedule 0, no INT32 copy) for a and w at any byte alignment
+// (gemm_bytes.hip): byte loads and the VALU's 4-way dot product; identical bits, slow.
+hipError_t launch_channel_gemm_bytes(const int8_t* a, const void* w, WeightCode code,
+                                     const float* sa, const void* sw, void* out, int m, int n,
+                                     int k, hipStream_t stream);
+
 // Small-M variant of launch_channel_gemm (gemm_small.hip): small output tiles, K split
 // over the workgroup's waves; identical bits. `cus` is the device's CU count.
 hipError_t launch_small_m_gemm(const int8_t* a, const void* w, WeightCode code, const float* sa,

@@ -114,7 +114,9 @@ int ci8_cutlass_channel_mm_noalloc(const int8_t* a, const int8_t* w, const float
 
 /* channel_mm: as fused_channel_mm with biased UINT8 weights w_u8 [n,k] holding
  * signed code + 128 (the weight used is w_u8 - 128). Any n > 0.
- * Requires m,n,k > 0, k % 32 == 0, k <= 65536, a and w <= INT_MAX elements.
+ * Requires m,n,k > 0, k % 32 == 0, k <= 65536, a and w <= INT_MAX elements; a and w
+ * may start at any byte (16-byte aligned operands run the MFMA kernels, others a slower
+ * byte-load kernel with the same bits), a_scale 4- and w_scale, out 2-byte aligned.
  * Replaces: channel_mm(const int8_t*, const uint8_t*, const float*, const void*, void*,
  *           int m, int n, int k, cudaStream_t), csrc/kernels.h:56-58;
  *           checks of csrc/bindings.cpp:252-258. */

@@ -72,6 +72,27 @@ def test_channel_mm_matches_integer_product_with_output_tails(ops, m, n, k):
     assert np.array_equal(bf16_bits(out), O.channel_mm(a_np, w_np, sa_np, sw_np))
 
 
+@pytest.mark.parametrize("a_off,w_off", [(1, 0), (0, 4), (3, 7), (16, 8)])
+@pytest.mark.parametrize("m,n,k", [(5, 70, 96), (130, 300, 544)])
+def test_channel_mm_accepts_operands_at_any_offset(ops, a_off, w_off, m, n, k):
+    """Operands sliced out of larger buffers at byte offsets the 16-byte copies cannot
+    take (csrc/bindings.cpp:238-265 accepts any view) run the byte-load kernel, with the
+    same bits as the oracle."""
+    rng = np.random.default_rng(a_off * 100 + w_off + m)
+    a_np, w_np, sa_np, sw_np = gemm_inputs(rng, m, n, k, biased=True)
+    a_buf = torch.zeros(m * k + 32, dtype=torch.int8, device="cuda")
+    w_buf = torch.zeros(n * k + 32, dtype=torch.uint8, device="cuda")
+    a = a_buf[a_off : a_off + m * k].view(m, k)
+    w = w_buf[w_off : w_off + n * k].view(n, k)
+    a.copy_(to_dev(a_np))
+    w.copy_(to_dev(w_np))
+    assert a.data_ptr() % 16 == a_off % 16 and w.data_ptr() % 16 == w_off % 16
+    out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    ops.channel_mm(a, w, to_dev(sa_np), to_dev(sw_np), out)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(out), O.channel_mm(a_np, w_np, sa_np, sw_np))
+
+
 def test_channel_mm_rejects_unaligned_k_before_launch(ops):
     with pytest.raises(RuntimeError, match="geometry"):
         ops.channel_mm(
