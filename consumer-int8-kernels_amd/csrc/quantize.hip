@@ -10,8 +10,8 @@
 // float->int conversion. The vector path takes the quotient from the row reciprocal and
 // divides only near half-integers (codes8 in ci8_device.h), with the same codes.
 //
-// Layout: one, two or four waves own a row (more for wider rows, so a lane holds at
-// most a few 16-byte packs) and keep it in registers between the max reduction and the
+// Layout: one, two or four waves own a row (four past 1024 values, so a lane holds
+// at most a few 16-byte packs) and keep it in registers between the max reduction and the
 // store, so HBM sees a single read of x and a single write of the codes, with 16-byte
 // loads and 8-byte nontemporal stores fully coalesced across the wave.
 #include "ci8_device.h"
@@ -116,15 +116,15 @@ hipError_t dispatch(const void* x, int8_t* codes, float* scales, int rows, int k
                                                          groups);                          \
     return hipGetLastError();                                                              \
   }
-  // Waves per row: enough that each lane holds at most a few 16-byte packs. Measured on
-  // [4096, 5120] this is about 25% faster than a whole row per wave (more waves keep more
-  // loads in flight, and a row's stores can start sooner).
+  // Waves per row: four once a row has four packs, so each lane holds at most a few
+  // 16-byte packs and a workgroup is one row. Measured on MI355X (us, 4 / 2 / 1 waves per
+  // row): [128, 4096] 3.04 / 4.05 / 7.33, [16, 5120] 3.76 / 5.20 / 8.12, [256, 5120]
+  // 3.37 / 4.31 / 7.11, [4096, 5120] 13.87 / 14.42 / 15.84: more waves keep more loads
+  // in flight and let a row's stores start sooner.
   if (vec) {
-    CI8_QW(1, 1) CI8_QW(1, 2) CI8_QW(1, 3) CI8_QW(1, 4)
-    CI8_QW(2, 3) CI8_QW(2, 4) CI8_QW(2, 5) CI8_QW(2, 6)
-    CI8_QW(4, 4) CI8_QW(4, 5) CI8_QW(4, 6) CI8_QW(4, 7) CI8_QW(4, 8) CI8_QW(4, 9)
-    CI8_QW(4, 10) CI8_QW(4, 12) CI8_QW(4, 14) CI8_QW(4, 16) CI8_QW(4, 20) CI8_QW(4, 24)
-    CI8_QW(4, 32)
+    CI8_QW(1, 1) CI8_QW(2, 1) CI8_QW(4, 1) CI8_QW(4, 2) CI8_QW(4, 3) CI8_QW(4, 4)
+    CI8_QW(4, 5) CI8_QW(4, 6) CI8_QW(4, 7) CI8_QW(4, 8) CI8_QW(4, 9) CI8_QW(4, 10)
+    CI8_QW(4, 12) CI8_QW(4, 14) CI8_QW(4, 16) CI8_QW(4, 20) CI8_QW(4, 24) CI8_QW(4, 32)
   }
 #undef CI8_QW
   quantize_rows_scalar_kernel<kGrouped><<<(rows + 3) / 4, 256, 0, stream>>>(
