@@ -11,7 +11,9 @@ rotate over enough copies that no step finds its inputs in the 256 MB Infinity C
 Also reported: `roofline` for the dominant kernel (the GEMM, timed per launch with HIP
 events on the stream it runs on); `mfma_probe`, the INT8 MFMA rate and shader clock
 under a full-chip pure-MFMA loop, with the dense INT8 peak at that measured clock
-(`roofline.frac_at_measured_clock` divides by it); `roofline.graph_median_us`, the GEMM
+(`roofline.frac_at_measured_clock` divides by it); `hbm_probe`, what plain streams of the
+GEMV's and the quantizer's bytes achieve (the HBM lines' `frac_of_stream` divides by
+it); `roofline.graph_median_us`, the GEMM
 timed as in the reference microbenchmark (graph replays of 10 launches, median); extra roofline lines for the quantizer, the W8A16
 GEMV, the grouped summed GEMM, the biased-UINT8 down
 projection with its SwiGLU activation producers (silu_mul_quantize,
@@ -161,6 +163,57 @@ def mfma_clock_probe(torch, cus: int, rounds: int = 4000, reps: int = 5) -> dict
     return {"tops": round(statistics.median(tops), 1), "clock_mhz": round(clock, 1),
             "clock_mhz_max": shader_khz.value / 1e3,
             "peak_at_clock_tops": round(cus * 8192 * clock * 1e6 / 1e12, 1)}
+
+
+def hbm_stream_probe(torch, cus: int) -> dict:
+    """Achievable HBM rates for the two traffic shapes of the HBM-bound kernels
+    (csrc/probe.hip): a plain read of the configs[1] weight bytes (K=5120, N=17408), and a
+    read of the configs[2] quantizer's BF16 input with a write of half as many bytes (its
+    codes), without the quantizer's per-row dependency. Rotated buffers larger than the
+    MALL; the best of three grid sizes, each timed as `time_kernel` times the ops."""
+    import ctypes
+
+    lib = ctypes.CDLL(str(REPO / "consumer-int8-kernels_amd" / "consumer_int8" / "libci8_probe.so"))
+    lib.ci8probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                         ctypes.c_int, ctypes.c_void_p]
+    lib.ci8probe_stream_read2_write1.argtypes = [ctypes.c_void_p, ctypes.c_int64,
+                                                 ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    stream = torch.cuda.current_stream().cuda_stream
+    out = {}
+    read_bytes = GEMV_N * GEMV_K
+    srcs = [torch.ones(read_bytes, dtype=torch.uint8, device="cuda") for _ in range(4)]
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    best = None
+    for blocks in (cus * 4, cus * 8, cus * 16):
+        calls = [lambda s=s, b=blocks: lib.ci8probe_stream_read(s.data_ptr(), read_bytes,
+                                                                sink.data_ptr(), b, stream)
+                 for s in srcs]
+        for c in calls:
+            assert c() == 0
+        mean_us, _ = time_kernel(torch, calls, 8)
+        if best is None or mean_us < best[0]:
+            best = (mean_us, blocks)
+    out["read"] = {"bytes": read_bytes, "mean_us": round(best[0], 2), "blocks": best[1],
+                   "gbs": round(read_bytes / (best[0] * 1e-6) / 1e9, 1)}
+    del srcs
+    rw_read = 2 * M * K
+    srcs = [torch.ones(rw_read, dtype=torch.uint8, device="cuda") for _ in range(6)]
+    dsts = [torch.empty(rw_read // 2, dtype=torch.uint8, device="cuda") for _ in range(6)]
+    best = None
+    for blocks in (cus * 4, cus * 8, cus * 16):
+        calls = [lambda s=s, d=d, b=blocks: lib.ci8probe_stream_read2_write1(
+                     s.data_ptr(), rw_read, d.data_ptr(), b, stream) for s, d in zip(srcs, dsts)]
+        for c in calls:
+            assert c() == 0
+        mean_us, _ = time_kernel(torch, calls, 8)
+        if best is None or mean_us < best[0]:
+            best = (mean_us, blocks)
+    rw_bytes = rw_read + rw_read // 2
+    out["read2_write1"] = {"bytes": rw_bytes, "mean_us": round(best[0], 2), "blocks": best[1],
+                           "gbs": round(rw_bytes / (best[0] * 1e-6) / 1e9, 1)}
+    del srcs, dsts
+    torch.cuda.synchronize()
+    return out
 
 
 def _cpu_model() -> str:
@@ -352,6 +405,10 @@ def main() -> int:
 
     if not args.no_extras:
         extras = {}
+        # What a pure stream of the same bytes achieves at these sizes: the practical
+        # ceiling for the HBM-bound lines below (their `frac_of_stream`).
+        hbm = hbm_stream_probe(torch, cus)
+        result["hbm_probe"] = hbm
         # quantize_rows [4096, 5120]: rotate 5 (x, codes) pairs = 315 MB > MALL.
         qx = [torch.randn(M, K, generator=gen, device="cuda").to(torch.bfloat16) for _ in range(5)]
         qc = [torch.empty(M, K, device="cuda", dtype=torch.int8) for _ in range(5)]
@@ -362,7 +419,8 @@ def main() -> int:
         gbs = QUANT_BYTES / (mean_us * 1e-6) / 1e9
         extras["quantize_rows"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                                    "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                                   "mean_us": round(mean_us, 2), "bytes": QUANT_BYTES}
+                                   "mean_us": round(mean_us, 2), "bytes": QUANT_BYTES,
+                                   "frac_of_stream": round(gbs / hbm["read2_write1"]["gbs"], 4)}
         del qx, qc
         # channel_gemv K=5120, N=17408: rotate 4 weight copies = 356 MB > MALL.
         gw = [torch.randint(-127, 128, (GEMV_N, GEMV_K), generator=gen, device="cuda",
@@ -379,7 +437,8 @@ def main() -> int:
             extras[f"channel_gemv_m{m}"] = {"bound": "hbm", "achieved": round(gbs, 1),
                                             "peak": PEAK_HBM_GBS, "unit": "GB/s",
                                             "frac": round(gbs / PEAK_HBM_GBS, 4),
-                                            "mean_us": round(mean_us, 2), "bytes": gemv_bytes(m)}
+                                            "mean_us": round(mean_us, 2), "bytes": gemv_bytes(m),
+                                            "frac_of_stream": round(gbs / hbm["read"]["gbs"], 4)}
         del gw, gs
         # grouped W8A8 summed over 4 groups of 4096, M=2048, N=4096 (4 weight
         # copies of 67 MB rotate, more than the MALL holds together with the codes).

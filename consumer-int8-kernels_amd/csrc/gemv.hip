@@ -27,9 +27,13 @@
 //  * One barrier per stage. The ring has three slots, held in three separate LDS
 //    arrays so the compiler can see that the slot being read is not the slot an
 //    in-flight copy is writing.
+// At m = 1 with K <= 8192 the MFMA would run 1 useful column of 16, and the weights
+// can stream in whole-row order instead: a row kernel (below) gives each wave whole
+// weight rows, read as 1 KiB contiguous pieces two rows ahead, and does the dequantize
+// and the dot product on the VALU (v_dot2_f32_bf16 on the BF16 products).
 // For K <= 8192 and 2 <= m <= 16, a balanced-span kernel (one 16-wave workgroup per
 // CU over an equal share of the channels, x fragments held in registers, W streamed one
-// block of 16 channels ahead) replaces the kernels below. At m = 1, and for longer K
+// block of 16 channels ahead) replaces the kernels below. At m = 1 for longer K
 // while x[0:m, :] fits in 64 KiB of LDS, a second kernel copies all of x into LDS once
 // and then lets every wave stream its W through a rolling window of ten 64-byte blocks
 // with no barriers at all, which removes the per-stage lock-step of the ring. Up to
@@ -482,6 +486,102 @@ __global__ void __launch_bounds__(C::kThreads, C::kWavesPerEU) channel_gemv_pers
 }
 
 // ---------------------------------------------------------------------------------
+// Row variant for m = 1: whole weight rows per wave, VALU dot products.
+//
+// Wave g of the grid (G waves) takes rows g, g + G, g + 2G, ...; a lane holds x[16 c'
+// + 0..15] for c' = 64 c + lane (kC = ceil(K / 1024) pieces of 1 KiB per row) in
+// registers, and each row arrives as kC 16-byte loads per lane, i.e. whole 1 KiB
+// pieces of one row per instruction (the order the memory system streams fastest).
+// Two rows are in flight: the loads of row r + 2G are issued right after row r's
+// products, so at each row the loads issued after its own are the next row's kC + 1
+// (codes and scale), and vmcnt(kC + 1) means row r has landed. A lane dequantizes its
+// 16 codes exactly as the MFMA kernels do (bf16_rn(code * scale), packed in pairs) and
+// feeds them with x to v_dot2_f32_bf16; the 64 lane sums meet by a butterfly, in FP32.
+// Rows past N load nothing (range-checked offsets) and store nothing.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+template <int kC>
+__global__ void __launch_bounds__(256) channel_gemv_rows_kernel(
+    const uint16_t* __restrict__ x, const int8_t* __restrict__ w,
+    const uint16_t* __restrict__ scale, uint16_t* __restrict__ out, int n, int k) {
+  constexpr int kAhead = 2;  // rows in flight per wave
+  const int lane = threadIdx.x & 63;
+  const int first = int(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int stride = int(gridDim.x) * 4;
+  const auto w_rsrc = make_rsrc(w, uint32_t(n) * uint32_t(k));
+  const auto x_rsrc = make_rsrc(x, uint32_t(k) * 2u);
+  const auto s_rsrc = make_rsrc(scale, uint32_t(n) * 2u);
+  u32x4 xv[kC][2];
+#pragma unroll
+  for (int c = 0; c < kC; ++c) {
+    const int col = c * 1024 + lane * 16;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      xv[c][h] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     x_rsrc, col < k ? uint32_t(col * 2 + h * 16) : kOutOfRange, 0, 0));
+  }
+  u32x4 wr[kAhead][kC];
+  uint32_t sr[kAhead];
+  auto issue = [&](int row, int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int c = 0; c < kC; ++c) {
+      const int col = c * 1024 + lane * 16;
+      wr[slot][c] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     w_rsrc, row < n && col < k ? uint32_t(row) * uint32_t(k) + uint32_t(col)
+                                                : kOutOfRange, 0, 0));
+    }
+    sr[slot] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, row < n ? uint32_t(row) * 2u
+                                                                   : kOutOfRange, 0, 0);
+  };
+#pragma unroll
+  for (int s = 0; s < kAhead; ++s) issue(first + s * stride, s);
+  for (int row0 = first; row0 < n; row0 += kAhead * stride) {  // uniform over the wave
+#pragma unroll
+    for (int s = 0; s < kAhead; ++s) {
+      const int row = row0 + s * stride;
+      waitcnt<vmcnt_imm((kAhead - 1) * (kC + 1))>();  // row `row` has landed
+      const float sc = bf16_to_f32(sr[s]);
+      float acc = 0.f;
+#pragma unroll
+      for (int c = 0; c < kC; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t word = wr[s][c][j];
+          const uint32_t p01 = pack_bf16x2(float(int8_t(word)) * sc, float(int8_t(word >> 8)) * sc);
+          const uint32_t p23 =
+              pack_bf16x2(float(int8_t(word >> 16)) * sc, float(int8_t(word >> 24)) * sc);
+          acc = dot2_bf16(p01, xv[c][j >> 1][2 * (j & 1)], acc);
+          acc = dot2_bf16(p23, xv[c][j >> 1][2 * (j & 1) + 1], acc);
+        }
+      issue(row + kAhead * stride, s);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+      if (lane == 0 && row < n) out[row] = uint16_t(f32_to_bf16(acc));
+    }
+  }
+  waitcnt<vmcnt_imm(0)>();  // drain the trailing (out-of-range) loads before exit
+}
+
+template <int kC>
+hipError_t run_rows(const void* x, const int8_t* w, const void* scale, void* out, int n, int k,
+                    int cus, hipStream_t stream) {
+  // Two waves per SIMD (measured best at N = 4096 .. 17408, K = 4096 .. 8192).
+  const int grid = max(1, min(cus * 2, (n + 3) / 4));
+  channel_gemv_rows_kernel<kC><<<grid, 256, 0, stream>>>(
+      static_cast<const uint16_t*>(x), w, static_cast<const uint16_t*>(scale),
+      static_cast<uint16_t*>(out), n, k);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------
 // Balanced-span variant: one 16-wave workgroup per CU, x in registers.
 //
 // Workgroup b owns the channel span [b * span, (b + 1) * span) with span = ceil(N /
@@ -634,9 +734,21 @@ hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale
                                int m, int n, int k, hipStream_t stream) {
   // K <= 8192 and m >= 2: the balanced-span kernel (measured on MI355X at K = 5120, N =
   // 17408: 20.2 - 22.9 us over m = 2 .. 16, against 20.4 - 30.9 us for the kernels below).
-  // At m = 1 the resident kernel, whose 32 waves per CU request almost all of their
-  // weights at once, stays about 1 us ahead (19.2 against 20.2 us).
   const int cus = device_cu_count();
+  // m = 1, K <= 8192: whole rows on the VALU (measured at K = 5120, N = 17408: 17.9 us
+  // against 21.2 us for the resident MFMA kernel under the same C-side launch loop).
+  if (m == 1 && cus > 0 && k <= 8192) {
+    switch ((k + 1023) / 1024) {
+      case 1: return run_rows<1>(x, w, scale, out, n, k, cus, stream);
+      case 2: return run_rows<2>(x, w, scale, out, n, k, cus, stream);
+      case 3: return run_rows<3>(x, w, scale, out, n, k, cus, stream);
+      case 4: return run_rows<4>(x, w, scale, out, n, k, cus, stream);
+      case 5: return run_rows<5>(x, w, scale, out, n, k, cus, stream);
+      case 6: return run_rows<6>(x, w, scale, out, n, k, cus, stream);
+      case 7: return run_rows<7>(x, w, scale, out, n, k, cus, stream);
+      default: return run_rows<8>(x, w, scale, out, n, k, cus, stream);
+    }
+  }
   const int range_len = ((k + 63) / 64 + 15) / 16;
   if (cus > 0 && range_len <= 8 && m >= 2) {
     if (range_len <= 2) return run_span<SpanConfig<2>>(x, w, scale, out, m, n, k, cus, stream);

@@ -1,4 +1,4 @@
-// Measurement helper for bench.py; not part of the drop-in library (it has no
+// Measurement helpers for bench.py; not part of the drop-in library (they have no
 // counterpart in the reference and no declaration in include/).
 //
 // A full-chip INT8 MFMA loop: one workgroup of 4 waves per CU, each wave running 8
@@ -59,9 +59,75 @@ __global__ void __launch_bounds__(256) mfma_loop_kernel(int rounds, int64_t* rec
   }
 }
 
+// HBM streaming references for the HBM-bound kernels: a plain read of `units` 16-byte
+// units (a weight stream), and a read of 16 bytes with a write of 8 per unit (the bytes
+// of a BF16 -> INT8 quantizer, without its per-row dependency). Each thread keeps 8 loads
+// in flight over a grid-stride loop; the loaded words are folded into a value that is
+// stored only if it matches a sentinel, so no load is dead.
+__global__ void __launch_bounds__(256) stream_read_kernel(const i32x4* __restrict__ src,
+                                                          int64_t units, int32_t* sink) {
+  const int64_t stride = int64_t(gridDim.x) * 256;
+  int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  int32_t fold = 0;
+  for (; i + 7 * stride < units; i += 8 * stride) {
+    i32x4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = src[i + j * stride];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) fold ^= v[j][0] ^ v[j][1] ^ v[j][2] ^ v[j][3];
+  }
+  for (; i < units; i += stride) {
+    const i32x4 v = src[i];
+    fold ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+  }
+  if (fold == 0x13579BDF) sink[0] = fold;
+}
+
+__global__ void __launch_bounds__(256) stream_read2_write1_kernel(const i32x4* __restrict__ src,
+                                                                  int64_t units,
+                                                                  int64_t* __restrict__ dst) {
+  const int64_t stride = int64_t(gridDim.x) * 256;
+  int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  for (; i + 7 * stride < units; i += 8 * stride) {
+    i32x4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = src[i + j * stride];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      __builtin_nontemporal_store(int64_t(uint32_t(v[j][0] ^ v[j][1])) |
+                                      int64_t(uint32_t(v[j][2] ^ v[j][3])) << 32,
+                                  dst + i + j * stride);
+  }
+  for (; i < units; i += stride) {
+    const i32x4 v = src[i];
+    __builtin_nontemporal_store(int64_t(uint32_t(v[0] ^ v[1])) | int64_t(uint32_t(v[2] ^ v[3])) << 32,
+                                dst + i);
+  }
+}
+
 }  // namespace
 
 extern "C" {
+
+// Reads `bytes` (a multiple of 16) from `src` with `blocks` workgroups of 256 threads.
+int ci8probe_stream_read(const void* src, int64_t bytes, int32_t* sink, int blocks, void* stream) {
+  if (src == nullptr || sink == nullptr || bytes <= 0 || bytes % 16 || blocks <= 0)
+    return int(hipErrorInvalidValue);
+  stream_read_kernel<<<blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const i32x4*>(src), bytes / 16, sink);
+  return int(hipGetLastError());
+}
+
+// Reads `bytes` (a multiple of 16) from `src` and writes bytes / 2 to `dst`.
+int ci8probe_stream_read2_write1(const void* src, int64_t bytes, void* dst, int blocks,
+                                 void* stream) {
+  if (src == nullptr || dst == nullptr || bytes <= 0 || bytes % 16 || blocks <= 0)
+    return int(hipErrorInvalidValue);
+  stream_read2_write1_kernel<<<blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const i32x4*>(src), bytes / 16, static_cast<int64_t*>(dst));
+  return int(hipGetLastError());
+}
+
 
 // MFMAs per wave per round, and INT8 ops per MFMA (16 x 16 x 64 x 2).
 int ci8probe_mfma_per_round(void) { return 32; }
