@@ -96,7 +96,10 @@ def test_long_k_kernels(ops, m, n, k):
     check_gemv(bf16_bits(out), x_bits, w, s_bits)
 
 
-@pytest.mark.parametrize("m,n,k", [(3, 100, 16), (5, 64, 48), (16, 7, 1040), (2, 33, 65536)])
+@pytest.mark.parametrize("m,n,k", [(3, 100, 16), (5, 64, 48), (16, 7, 1040), (2, 33, 65536),
+                                   # m = 1 row kernel: one 16-value piece, the longest K it
+                                   # takes, more rows than waves with a ragged last piece
+                                   (1, 7, 16), (1, 33, 8192), (1, 20003, 1040)])
 def test_gemv_tails_and_unaligned_activations(ops, m, n, k):
     rng = np.random.default_rng(m * n + k)
     x_bits = randn_bf16(rng, (m, k))
