@@ -12,18 +12,28 @@
 //
 // The integer accumulation restarts every 32 values of K, so each block is one
 // v_mfma_i32_16x16x32_i8 into a zeroed accumulator followed by the FP32 rescale of its
-// 4 outputs per lane: a convert, the scale product and a multiply-add, 3 VALU
-// instructions per output per block. That rescale, not the matrix cores, bounds the
-// kernel: one 16x16x32 MFMA (8 K of MAC per lane-cycle) against 12 VALU instructions.
+// 4 outputs per lane.
 //
-// Layout: a workgroup computes a 64 x 64 output tile on 8 waves (16 rows x 32 columns
-// each: 1 x 2 MFMA tiles), or 32 x 32 on 4 waves for small problems. K advances 256
+// Main kernel (K a multiple of 128, sw 4-byte aligned): A, W and both scale arrays go
+// through a four-stage LDS ring filled by buffer_load ... lds (three stages in flight
+// per workgroup), 128 K values (4 blocks) a stage. The scale products fl(sa * sw) of a
+// stage's 4 blocks come from one v_mfma_f32_16x16x1f32 per 16 x 16 tile: its four
+// 16 x 16 outer products (A column = sa of block lane / 16, B row = sw of that block)
+// are exact products rounded once each, as the FP32 multiply rounds (checked on MI355X
+// over 4.2 M operand pairs: identical bits, except that a zero product is +0 where the
+// multiply gives -0, which cannot reach the output because the running sum, starting
+// at +0, is never -0), and they land in the layout of the INT32 MFMA output. That
+// leaves 2 VALU instructions per output per block (a convert and the multiply-add).
+// Tiles: 64 x 64 on 8 waves (2 x 4 waves of 32 x 16), or 128 x 128 on 16 waves once
+// those fill the chip twice over. Measured on MI355X: M=2048, N=1024, K=4096 56 -> 38
+// us, M=N=K=4096 366 -> 257 us against the kernel below.
+//
+// Fallback (any K % 32 == 0): a workgroup computes a 64 x 64 output tile on 8 waves
+// (16 rows x 32 columns each), or 32 x 32 on 4 waves for small problems. K advances 256
 // values (8 blocks) a step: the A and W slabs (16-byte loads, rows padded in LDS against
 // bank conflicts) and their scales (W's converted to FP32) are staged in LDS, with the
-// next step's global loads issued into registers before the current step's arithmetic.
-// Measured at M=2048, N=1024, K=4096: 55 us, 37% of the VALU bound of the rescale; the
-// LDS reads (operands and scales, about 5 bytes per output per block) run close to their
-// own limit beside it.
+// next step's global loads issued into registers before the current step's arithmetic,
+// and the scale product is a VALU multiply (3 VALU instructions per output per block).
 #include "ci8_device.h"
 #include "launch.h"
 
@@ -221,7 +231,8 @@ __global__ void __launch_bounds__(64 * kWR * kWC, kOcc) q8_block_mm_kernel(
   __shared__ Lds<T> lds;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int row0 = blockIdx.y * T::kBM, col0 = blockIdx.x * T::kBN;
+  const int tiles_n = (n + T::kBN - 1) / T::kBN;
+  const int row0 = int(blockIdx.x) / tiles_n * T::kBM, col0 = int(blockIdx.x) % tiles_n * T::kBN;
   const int wrow = (wave / kWC) * kWM * 16, wcol = (wave % kWC) * kWN * 16;
 
   float sum[kWM][kWN][4];
@@ -264,10 +275,210 @@ template <int kWR, int kWC, int kWM, int kWN, int kBK, int kOcc, int kUnroll>
 void launch_q8_tile(const int8_t* a, const float* sa, const int8_t* w, const uint16_t* sw,
                     uint16_t* y, int m, int n, int k, hipStream_t stream) {
   using T = Q8Tile<kWR, kWC, kWM, kWN, kBK>;
-  const dim3 grid((n + T::kBN - 1) / T::kBN, (m + T::kBM - 1) / T::kBM);
+  // One-dimensional grid: m * n <= INT_MAX keeps the tile count far below 2^31 - 1.
+  const unsigned grid = unsigned((n + T::kBN - 1) / T::kBN) * unsigned((m + T::kBM - 1) / T::kBM);
   q8_block_mm_kernel<kWR, kWC, kWM, kWN, kBK, kOcc, kUnroll>
       <<<grid, T::kThreads, 0, stream>>>(a, sa, w, sw, y, m, n, k);
 }
+
+// ------------------------------------------------------------------ ring kernel
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// LDS DMA copies (non-template helpers: the host pass of a kernel template rejects the
+// 16-byte form of the builtin, which only gfx950 has).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, lds_void* dst,
+                                      uint32_t offset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, offset, 0, 0, 0);
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t rsrc, lds_void* dst,
+                                     uint32_t offset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 4, offset, 0, 0, 0);
+}
+
+// kWM x kWN waves, each owning kTM x kTN MFMA tiles of 16 x 16; kNS ring stages of
+// 128 K values; kOcc waves per SIMD the register allocation must allow.
+template <int kWM_, int kWN_, int kTM_, int kTN_, int kNS_, int kOcc_>
+struct RingTile {
+  static constexpr int kWM = kWM_, kWN = kWN_, kTM = kTM_, kTN = kTN_, kNS = kNS_;
+  static constexpr int kOcc = kOcc_;
+  static constexpr int kWaves = kWM * kWN, kThreads = 64 * kWaves;
+  static constexpr int kBM = kWM * kTM * 16, kBN = kWN * kTN * 16, kBK = 128;
+  // One stage: A rows of 128 bytes, W rows, sa [row][4 blocks] FP32, and sw as two
+  // planes (blocks 0-1, 2-3) of [column][2 blocks] FP16.
+  static constexpr int kA = kBM * kBK, kW = kBN * kBK, kSa = kBM * 16, kSw = kBN * 8;
+  static constexpr int kStage = kA + kW + kSa + kSw;
+  // Copies per stage: 1 KiB of A or W rows (8 rows x 128 bytes), 1 KiB of sa (64 rows),
+  // 256 bytes of one sw plane (64 columns x 4 bytes).
+  static constexpr int nA = kBM / 8, nW = kBN / 8, nSa = kBM / 64, nSw = kBN / 32;
+  static constexpr int nCopies = nA + nW + nSa + nSw;
+  static constexpr int kPerWave = (nCopies + kWaves - 1) / kWaves;  // the rest: junk copies
+  static constexpr int kJunk = kNS * kStage;
+  static constexpr int kLds = kJunk + 1024;
+  static_assert(kBM % 64 == 0 && kBN % 64 == 0, "scale copies cover 64 rows or columns");
+  static_assert(kLds <= 160 * 1024, "LDS");
+  static_assert(kPerWave * (kNS - 2) <= 63, "vmcnt holds 6 bits");
+};
+
+// Requires k % 128 == 0, a and w 16-byte aligned, sa 4-byte and sw 4-byte aligned.
+// A and W rows sit in LDS with their 16-byte chunks XOR-swizzled by row % 8.
+template <class T>
+__global__ void __launch_bounds__(T::kThreads, T::kOcc) q8_ring_kernel(
+    const int8_t* __restrict__ a, const float* __restrict__ sa, const int8_t* __restrict__ w,
+    const uint16_t* __restrict__ sw, uint16_t* __restrict__ y, int m, int n, int k) {
+  extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
+  auto* lds = (char __attribute__((address_space(3)))*)(lds_raw);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tiles_n = (n + T::kBN - 1) / T::kBN;
+  const int row0 = int(blockIdx.x) / tiles_n * T::kBM, col0 = int(blockIdx.x) % tiles_n * T::kBN;
+  const int kb32 = k / 32;
+  const int stages = k / T::kBK;
+  const auto a_rsrc = make_rsrc(a, uint32_t(m) * uint32_t(k));
+  const auto w_rsrc = make_rsrc(w, uint32_t(n) * uint32_t(k));
+  const auto sa_rsrc = make_rsrc(sa, uint32_t(m) * uint32_t(kb32) * 4u);
+  const auto sw_rsrc = make_rsrc(sw, uint32_t(n) * uint32_t(kb32) * 2u);
+
+  // Stage st's copies into ring slot st % kNS: copy j = wave + kWaves * i of the list
+  // A, W, sa, sw, junk (every wave issues kPerWave, so one vmcnt fits all). Stages past
+  // the end copy nothing but zeros from out of range, which keeps the counts uniform.
+  auto issue = [&](int st) __attribute__((always_inline)) {
+    const int slot = (st % T::kNS) * T::kStage;
+    const bool live = st < stages;
+    const uint32_t kb = uint32_t(st) * T::kBK;
+#pragma unroll
+    for (int i = 0; i < T::kPerWave; ++i) {
+      const int j = wave + T::kWaves * i;  // uniform over the wave
+      if (j < T::nA + T::nW) {
+        const bool is_a = j < T::nA;
+        const int jj = is_a ? j : j - T::nA;
+        const int r = jj * 8 + (lane >> 3);
+        const int chunk = (lane & 7) ^ (r & 7);
+        const int first = is_a ? row0 : col0;
+        const bool valid = live && first + r < (is_a ? m : n);
+        dma16(is_a ? a_rsrc : w_rsrc,
+              (lds_void*)(lds + slot + (is_a ? 0 : T::kA) + jj * 1024),
+              valid ? uint32_t(first + r) * uint32_t(k) + kb + uint32_t(chunk * 16) : kOutOfRange);
+      } else if (j < T::nA + T::nW + T::nSa) {
+        const int jj = j - T::nA - T::nW;
+        const int r = jj * 64 + lane;
+        const bool valid = live && row0 + r < m;
+        dma16(sa_rsrc, (lds_void*)(lds + slot + T::kA + T::kW + jj * 1024),
+              valid ? uint32_t(row0 + r) * uint32_t(kb32) * 4u + kb / 8 : kOutOfRange);
+      } else if (j < T::nCopies) {
+        const int jj = j - T::nA - T::nW - T::nSa;  // plane jj % 2, columns 64 (jj / 2) ..
+        const int plane = jj & 1, c = (jj >> 1) * 64 + lane;
+        const bool valid = live && col0 + c < n;
+        dma4(sw_rsrc,
+             (lds_void*)(lds + slot + T::kA + T::kW + T::kSa + plane * (T::kBN * 4) + (jj >> 1) * 256),
+             valid ? uint32_t(col0 + c) * uint32_t(kb32) * 2u + kb / 16 + 4u * plane : kOutOfRange);
+      } else {
+        dma4(sw_rsrc, (lds_void*)(lds + T::kJunk), kOutOfRange);
+      }
+    }
+  };
+
+  const int wm = wave % T::kWM, wn = wave / T::kWM;
+  const int lr = lane & 15, lq = lane >> 4;
+  float sum[T::kTM][T::kTN][4];
+#pragma unroll
+  for (int ti = 0; ti < T::kTM; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < T::kTN; ++tj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sum[ti][tj][i] = 0.f;
+
+#pragma unroll
+  for (int st = 0; st < T::kNS - 1; ++st) issue(st);
+  for (int t = 0; t < stages; ++t) {
+    // This wave's copies of stage t have landed (those of the kNS - 2 later stages may
+    // be in flight); after the barrier every wave's have, and slot (t - 1) % kNS, read
+    // in stage t - 1, is free for stage t + kNS - 1.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(T::kPerWave * (T::kNS - 2)));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(t + T::kNS - 1);
+    __builtin_amdgcn_sched_barrier(0);
+    const auto* base = lds + (t % T::kNS) * T::kStage;
+    f32x16_t scl[T::kTM][T::kTN];
+    {
+      float sa_op[T::kTM], sw_op[T::kTN];
+#pragma unroll
+      for (int ti = 0; ti < T::kTM; ++ti) {
+        const int row = (wm * T::kTM + ti) * 16 + lr;
+        sa_op[ti] = *reinterpret_cast<const __attribute__((address_space(3))) float*>(
+            base + T::kA + T::kW + row * 16 + lq * 4);
+      }
+#pragma unroll
+      for (int tj = 0; tj < T::kTN; ++tj) {
+        const int col = (wn * T::kTN + tj) * 16 + lr;
+        sw_op[tj] = half_to_float(*reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(
+            base + T::kA + T::kW + T::kSa + (lq >> 1) * (T::kBN * 4) + col * 4 + (lq & 1) * 2));
+      }
+#pragma unroll
+      for (int ti = 0; ti < T::kTM; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < T::kTN; ++tj)
+          scl[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x1f32(sa_op[ti], sw_op[tj], f32x16_t{}, 0, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      // Lane group lq takes bytes 8 lq .. 8 lq + 7 of block q: chunk 2q + lq / 2.
+      const int chunk = 2 * q + (lq >> 1);
+      int64_t af[T::kTM], wf[T::kTN];
+#pragma unroll
+      for (int ti = 0; ti < T::kTM; ++ti) {
+        const int row = (wm * T::kTM + ti) * 16 + lr;
+        af[ti] = *reinterpret_cast<const __attribute__((address_space(3))) int64_t*>(
+            base + row * 128 + ((chunk ^ (row & 7)) * 16) + (lq & 1) * 8);
+      }
+#pragma unroll
+      for (int tj = 0; tj < T::kTN; ++tj) {
+        const int row = (wn * T::kTN + tj) * 16 + lr;
+        wf[tj] = *reinterpret_cast<const __attribute__((address_space(3))) int64_t*>(
+            base + T::kA + row * 128 + ((chunk ^ (row & 7)) * 16) + (lq & 1) * 8);
+      }
+#pragma unroll
+      for (int ti = 0; ti < T::kTM; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < T::kTN; ++tj) {
+          const i32x4_t acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[ti], wf[tj],
+                                                                   i32x4_t{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            sum[ti][tj][i] = __builtin_fmaf(float(acc[i]), scl[ti][tj][4 * q + i], sum[ti][tj][i]);
+        }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // drain the trailing (out-of-range) copies
+#pragma unroll
+  for (int ti = 0; ti < T::kTM; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < T::kTN; ++tj) {
+      const int col = col0 + (wn * T::kTN + tj) * 16 + lr;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = row0 + (wm * T::kTM + ti) * 16 + lq * 4 + i;
+        if (row < m && col < n) y[int64_t(row) * n + col] = uint16_t(f32_to_bf16(sum[ti][tj][i]));
+      }
+    }
+}
+
+template <class T>
+hipError_t launch_ring(const int8_t* a, const float* sa, const int8_t* w, const uint16_t* sw,
+                       uint16_t* y, int m, int n, int k, hipStream_t stream) {
+  auto kernel = q8_ring_kernel<T>;
+  static std::atomic<bool> configured{false};
+  if (const hipError_t e = raise_lds_limit_once(kernel, T::kLds, configured); e != hipSuccess)
+    return e;
+  // One-dimensional grid: m * n <= INT_MAX keeps the tile count far below 2^31 - 1.
+  const unsigned grid = unsigned((m + T::kBM - 1) / T::kBM) * unsigned((n + T::kBN - 1) / T::kBN);
+  kernel<<<grid, T::kThreads, T::kLds, stream>>>(a, sa, w, sw, y, m, n, k);
+  return hipGetLastError();
+}
+
+using Ring64 = RingTile<2, 4, 2, 1, 4, 2>;   // 64 x 64, waves of 32 x 16, two per CU
+using Ring128 = RingTile<4, 4, 2, 2, 4, 4>;  // 128 x 128 on 16 waves, one per CU
 
 }  // namespace
 
@@ -293,6 +504,15 @@ hipError_t launch_q8_block_mm(const int8_t* a, const float* sa, const int8_t* w,
   // K = 4096, M = 512 and 2048).
   const auto* s16 = static_cast<const uint16_t*>(sw);
   auto* out = static_cast<uint16_t*>(y);
+  if (k % 128 == 0 && reinterpret_cast<uintptr_t>(sw) % 4 == 0) {
+    // The ring kernel; 128 x 128 tiles once there are two per CU (M = N = K = 4096: 257
+    // against 272 us for 64 x 64), else 64 x 64.
+    const int cus = device_cu_count();
+    const int64_t tiles128 = int64_t((m + 127) / 128) * ((n + 127) / 128);
+    if (cus > 0 && tiles128 >= 2 * int64_t(cus))
+      return launch_ring<Ring128>(a, sa, w, s16, out, m, n, k, stream);
+    return launch_ring<Ring64>(a, sa, w, s16, out, m, n, k, stream);
+  }
   const int64_t big_tiles = int64_t((m + 63) / 64) * ((n + 63) / 64);
   if (big_tiles >= 256)
     launch_q8_tile<4, 2, 1, 2, 256, 4, 2>(a, sa, w, s16, out, m, n, k, stream);

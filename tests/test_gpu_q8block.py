@@ -166,3 +166,60 @@ def test_q8_block_special_values(lib):
     got = bf16_bits(y)
     same = (got == expected) | (np.isnan(O.bf16_to_f32(got)) & np.isnan(O.bf16_to_f32(expected)))
     assert same.all()
+
+
+@pytest.mark.parametrize("m,n,k", [(100, 70, 384), (65, 129, 128), (300, 200, 1024),
+                                   (2048, 4096, 256), (2000, 4100, 128)])
+def test_q8_block_ring_tiles(lib, m, n, k):
+    """K a multiple of 128 takes the LDS-ring kernel: 64 x 64 tiles, and 128 x 128 tiles
+    once there are two per CU (the last two shapes on a 256-CU GPU, the second with
+    ragged row and column tiles). Bit-exact against the oracle."""
+    x_bits, w, sw = make_case(m, n, k, 71 + m + n + k)
+    a, sa, y = run_fused(lib, to_dev(x_bits), to_dev(w), to_dev(sw), m, n, k)
+    torch.cuda.synchronize()
+    check_against_oracle(x_bits, w, sw, a, sa, y)
+
+
+def test_q8_block_ring_needs_aligned_scales(lib):
+    """Block scales two bytes off 4-byte alignment take the step kernel, same bits."""
+    m, n, k = 70, 90, 256
+    x_bits, w, sw = make_case(m, n, k, 13)
+    storage = to_dev(np.concatenate([np.zeros(1, np.uint16), sw.reshape(-1)]))
+    sw_odd = storage[1:].view(n, k // 32)
+    a = torch.empty(m, k, device="cuda", dtype=torch.int8)
+    sa = torch.empty(m, k // 32, device="cuda", dtype=torch.float32)
+    y = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    dx, dw = to_dev(x_bits), to_dev(w)
+    assert lib.ci8_q8_block_int8(dx.data_ptr(), a.data_ptr(), sa.data_ptr(), dw.data_ptr(),
+                                 sw_odd.data_ptr(), y.data_ptr(), m, n, k, stream()) == 0
+    torch.cuda.synchronize()
+    check_against_oracle(x_bits, w, sw, a, sa, y)
+    a2, sa2, y2 = run_fused(lib, dx, dw, to_dev(sw), m, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+
+
+def test_q8_block_ring_special_values(lib):
+    """Infinite and NaN activations and zero or negative-zero weight scales through the
+    ring kernel (its scale products come from an MFMA outer product): the same values as
+    the oracle, NaN for NaN."""
+    m, n, k = 24, 40, 256
+    x_bits, w, sw = make_case(m, n, k, 21)
+    vals = O.bf16_to_f32(x_bits).copy()
+    vals[1, 140] = np.inf
+    vals[2, 5] = np.nan
+    vals[3, 200] = -np.inf
+    x_bits = O.f32_to_bf16(vals)
+    sw = sw.copy()
+    sw[0, :] = 0x0000
+    sw[1, 2] = 0x8000
+    sw[2, 3] = 0x0001  # the smallest FP16 subnormal
+    a, sa, y = run_fused(lib, to_dev(x_bits), to_dev(w), to_dev(sw), m, n, k)
+    torch.cuda.synchronize()
+    oa, osa = O.quantize_block32(x_bits)
+    assert np.array_equal(host(sa), osa) and np.array_equal(host(a), oa)
+    with np.errstate(invalid="ignore", over="ignore"):
+        expected = O.q8_block_mm(oa, osa, w, sw)
+    got = bf16_bits(y)
+    same = (got == expected) | (np.isnan(O.bf16_to_f32(got)) & np.isnan(O.bf16_to_f32(expected)))
+    assert same.all()
