@@ -321,7 +321,10 @@ struct RingTile {
 };
 
 // Requires k % 128 == 0, a and w 16-byte aligned, sa 4-byte and sw 4-byte aligned.
-// A and W rows sit in LDS with their 16-byte chunks XOR-swizzled by row % 8.
+// A and W rows sit in LDS with their 16-byte chunks XOR-swizzled by (row / 2) % 8: a
+// fragment read (16 rows x 8 bytes per half-wave, rows 256 bytes = all 64 banks apart
+// every two rows) then touches each bank once, where row % 8 puts rows r and r + 8 on
+// the same banks.
 template <class T>
 __global__ void __launch_bounds__(T::kThreads, T::kOcc) q8_ring_kernel(
     const int8_t* __restrict__ a, const float* __restrict__ sa, const int8_t* __restrict__ w,
@@ -353,7 +356,7 @@ __global__ void __launch_bounds__(T::kThreads, T::kOcc) q8_ring_kernel(
         const bool is_a = j < T::nA;
         const int jj = is_a ? j : j - T::nA;
         const int r = jj * 8 + (lane >> 3);
-        const int chunk = (lane & 7) ^ (r & 7);
+        const int chunk = (lane & 7) ^ ((r >> 1) & 7);
         const int first = is_a ? row0 : col0;
         const bool valid = live && first + r < (is_a ? m : n);
         dma16(is_a ? a_rsrc : w_rsrc,
@@ -430,13 +433,13 @@ __global__ void __launch_bounds__(T::kThreads, T::kOcc) q8_ring_kernel(
       for (int ti = 0; ti < T::kTM; ++ti) {
         const int row = (wm * T::kTM + ti) * 16 + lr;
         af[ti] = *reinterpret_cast<const __attribute__((address_space(3))) int64_t*>(
-            base + row * 128 + ((chunk ^ (row & 7)) * 16) + (lq & 1) * 8);
+            base + row * 128 + ((chunk ^ ((row >> 1) & 7)) * 16) + (lq & 1) * 8);
       }
 #pragma unroll
       for (int tj = 0; tj < T::kTN; ++tj) {
         const int row = (wn * T::kTN + tj) * 16 + lr;
         wf[tj] = *reinterpret_cast<const __attribute__((address_space(3))) int64_t*>(
-            base + T::kA + row * 128 + ((chunk ^ (row & 7)) * 16) + (lq & 1) * 8);
+            base + T::kA + row * 128 + ((chunk ^ ((row >> 1) & 7)) * 16) + (lq & 1) * 8);
       }
 #pragma unroll
       for (int ti = 0; ti < T::kTM; ++ti)

@@ -70,7 +70,7 @@ def test_balanced_spans(ops, m, n, k):
     """K <= 8192 (m >= 2) runs one workgroup per CU over equal channel spans (N = 17408:
     68 per CU): fewer channels than CUs x 16, spans that end inside a block of 16, more
     than 8 blocks per span (two partial-sum batches), every x-register configuration (K
-    ranges of 2, 4, 5 and 8 blocks of 64) and a K tail; m = 1 takes the resident kernel."""
+    ranges of 2, 4, 5 and 8 blocks of 64) and a K tail; m = 1 takes the row kernel."""
     rng = np.random.default_rng(m * 7 + n + k)
     x_bits = randn_bf16(rng, (m, k))
     w = rng.integers(-128, 128, (n, k)).astype(np.int8)
