@@ -345,39 +345,65 @@ __global__ void __launch_bounds__(T::kThreads, T::kOcc) q8_ring_kernel(
   // Stage st's copies into ring slot st % kNS: copy j = wave + kWaves * i of the list
   // A, W, sa, sw, junk (every wave issues kPerWave, so one vmcnt fits all). Stages past
   // the end copy nothing but zeros from out of range, which keeps the counts uniform.
+  // Each of this wave's copies is fixed up front as (buffer, LDS offset in the slot,
+  // this lane's offset at stage 0 or out of range, bytes per stage, 16 or 4 bytes per
+  // lane), so a stage issues them without walking the list.
+  __amdgpu_buffer_rsrc_t c_rsrc[T::kPerWave];
+  int c_lds[T::kPerWave];
+  uint32_t c_off[T::kPerWave], c_step[T::kPerWave];
+  bool c_wide[T::kPerWave];
+#pragma unroll
+  for (int i = 0; i < T::kPerWave; ++i) {
+    const int j = wave + T::kWaves * i;  // uniform over the wave
+    if (j < T::nA + T::nW) {
+      const bool is_a = j < T::nA;
+      const int jj = is_a ? j : j - T::nA;
+      const int r = jj * 8 + (lane >> 3);
+      const int chunk = (lane & 7) ^ ((r >> 1) & 7);
+      const int first = is_a ? row0 : col0;
+      c_rsrc[i] = is_a ? a_rsrc : w_rsrc;
+      c_lds[i] = (is_a ? 0 : T::kA) + jj * 1024;
+      c_off[i] = first + r < (is_a ? m : n) ? uint32_t(first + r) * uint32_t(k) + uint32_t(chunk * 16)
+                                            : kOutOfRange;
+      c_step[i] = T::kBK;
+      c_wide[i] = true;
+    } else if (j < T::nA + T::nW + T::nSa) {
+      const int jj = j - T::nA - T::nW;
+      const int r = jj * 64 + lane;
+      c_rsrc[i] = sa_rsrc;
+      c_lds[i] = T::kA + T::kW + jj * 1024;
+      c_off[i] = row0 + r < m ? uint32_t(row0 + r) * uint32_t(kb32) * 4u : kOutOfRange;
+      c_step[i] = 16;  // 4 blocks x FP32
+      c_wide[i] = true;
+    } else if (j < T::nCopies) {
+      const int jj = j - T::nA - T::nW - T::nSa;  // plane jj % 2, columns 64 (jj / 2) ..
+      const int plane = jj & 1, c = (jj >> 1) * 64 + lane;
+      c_rsrc[i] = sw_rsrc;
+      c_lds[i] = T::kA + T::kW + T::kSa + plane * (T::kBN * 4) + (jj >> 1) * 256;
+      c_off[i] = col0 + c < n ? uint32_t(col0 + c) * uint32_t(kb32) * 2u + 4u * plane : kOutOfRange;
+      c_step[i] = 8;  // 4 blocks x FP16
+      c_wide[i] = false;
+    } else {
+      c_rsrc[i] = sw_rsrc;
+      c_lds[i] = -1;  // the junk KiB, outside the ring
+      c_off[i] = kOutOfRange;
+      c_step[i] = 0;
+      c_wide[i] = false;
+    }
+  }
   auto issue = [&](int st) __attribute__((always_inline)) {
     const int slot = (st % T::kNS) * T::kStage;
     const bool live = st < stages;
-    const uint32_t kb = uint32_t(st) * T::kBK;
 #pragma unroll
     for (int i = 0; i < T::kPerWave; ++i) {
-      const int j = wave + T::kWaves * i;  // uniform over the wave
-      if (j < T::nA + T::nW) {
-        const bool is_a = j < T::nA;
-        const int jj = is_a ? j : j - T::nA;
-        const int r = jj * 8 + (lane >> 3);
-        const int chunk = (lane & 7) ^ ((r >> 1) & 7);
-        const int first = is_a ? row0 : col0;
-        const bool valid = live && first + r < (is_a ? m : n);
-        dma16(is_a ? a_rsrc : w_rsrc,
-              (lds_void*)(lds + slot + (is_a ? 0 : T::kA) + jj * 1024),
-              valid ? uint32_t(first + r) * uint32_t(k) + kb + uint32_t(chunk * 16) : kOutOfRange);
-      } else if (j < T::nA + T::nW + T::nSa) {
-        const int jj = j - T::nA - T::nW;
-        const int r = jj * 64 + lane;
-        const bool valid = live && row0 + r < m;
-        dma16(sa_rsrc, (lds_void*)(lds + slot + T::kA + T::kW + jj * 1024),
-              valid ? uint32_t(row0 + r) * uint32_t(kb32) * 4u + kb / 8 : kOutOfRange);
-      } else if (j < T::nCopies) {
-        const int jj = j - T::nA - T::nW - T::nSa;  // plane jj % 2, columns 64 (jj / 2) ..
-        const int plane = jj & 1, c = (jj >> 1) * 64 + lane;
-        const bool valid = live && col0 + c < n;
-        dma4(sw_rsrc,
-             (lds_void*)(lds + slot + T::kA + T::kW + T::kSa + plane * (T::kBN * 4) + (jj >> 1) * 256),
-             valid ? uint32_t(col0 + c) * uint32_t(kb32) * 2u + kb / 16 + 4u * plane : kOutOfRange);
-      } else {
-        dma4(sw_rsrc, (lds_void*)(lds + T::kJunk), kOutOfRange);
-      }
+      const uint32_t off =
+          live && c_off[i] != kOutOfRange ? c_off[i] + uint32_t(st) * c_step[i] : kOutOfRange;
+      auto* dst = (lds_void*)(lds + (c_lds[i] < 0 ? T::kJunk : slot + c_lds[i]));
+      // A copy slot that holds A, W or sa rows for every wave needs no branch.
+      if ((i + 1) * T::kWaves <= T::nA + T::nW + T::nSa || c_wide[i])
+        dma16(c_rsrc[i], dst, off);
+      else
+        dma4(c_rsrc[i], dst, off);
     }
   };
 
