@@ -321,10 +321,10 @@ struct RingTile {
 };
 
 // Requires k % 128 == 0, a and w 16-byte aligned, sa 4-byte and sw 4-byte aligned.
-// A and W rows sit in LDS with their 16-byte chunks XOR-swizzled by (row / 2) % 8: a
-// fragment read (16 rows x 8 bytes per half-wave, rows 256 bytes = all 64 banks apart
-// every two rows) then touches each bank once, where row % 8 puts rows r and r + 8 on
-// the same banks.
+// A and W rows sit in LDS with their 16-byte chunks XOR-swizzled by (row / 2) % 8. The
+// 8-byte fragment reads of 16 rows still meet 2-way bank conflicts (the copies move
+// 16-byte chunks, so no swizzle can separate the two 8-byte halves of a chunk):
+// measured on MI355X, 17.8% of the kernel's cycles against 21.8% with row % 8.
 template <class T>
 __global__ void __launch_bounds__(T::kThreads, T::kOcc) q8_ring_kernel(
     const int8_t* __restrict__ a, const float* __restrict__ sa, const int8_t* __restrict__ w,
