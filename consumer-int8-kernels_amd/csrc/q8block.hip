@@ -284,6 +284,8 @@ void launch_q8_tile(const int8_t* a, const float* sa, const int8_t* w, const uin
 // ------------------------------------------------------------------ ring kernel
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x32_t __attribute__((ext_vector_type(32)));
+typedef int32_t i32x16_t __attribute__((ext_vector_type(16)));
 
 // LDS DMA copies (non-template helpers: the host pass of a kernel template rejects the
 // 16-byte form of the builtin, which only gfx950 has).
@@ -296,12 +298,15 @@ __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t rsrc, lds_void* dst,
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 4, offset, 0, 0, 0);
 }
 
-// kWM x kWN waves, each owning kTM x kTN MFMA tiles of 16 x 16; kNS ring stages of
-// 128 K values; kOcc waves per SIMD the register allocation must allow.
-template <int kWM_, int kWN_, int kTM_, int kTN_, int kNS_, int kOcc_>
+// kWM x kWN waves, each owning kTM x kTN MFMA tiles of 16 x 16 (or, with kMfma32, one
+// 32 x 32 tile: kTM = kTN = 2); kNS ring stages of 128 K values; kOcc waves per SIMD
+// the register allocation must allow.
+template <int kWM_, int kWN_, int kTM_, int kTN_, int kNS_, int kOcc_, bool kMfma32_ = false>
 struct RingTile {
   static constexpr int kWM = kWM_, kWN = kWN_, kTM = kTM_, kTN = kTN_, kNS = kNS_;
   static constexpr int kOcc = kOcc_;
+  static constexpr bool kMfma32 = kMfma32_;
+  static_assert(!kMfma32 || (kTM == 2 && kTN == 2), "a 32 x 32 tile per wave");
   static constexpr int kWaves = kWM * kWN, kThreads = 64 * kWaves;
   static constexpr int kBM = kWM * kTM * 16, kBN = kWN * kTN * 16, kBK = 128;
   // One stage: A rows of 128 bytes, W rows, sa [row][4 blocks] FP32, and sw as two
@@ -321,10 +326,19 @@ struct RingTile {
 };
 
 // Requires k % 128 == 0, a and w 16-byte aligned, sa 4-byte and sw 4-byte aligned.
-// A and W rows sit in LDS with their 16-byte chunks XOR-swizzled by (row / 2) % 8. The
-// 8-byte fragment reads of 16 rows still meet 2-way bank conflicts (the copies move
-// 16-byte chunks, so no swizzle can separate the two 8-byte halves of a chunk):
-// measured on MI355X, 17.8% of the kernel's cycles against 21.8% with row % 8.
+// 16 x 16 tiles: v_mfma_i32_16x16x32_i8, one per block, reads 8 bytes a lane; A and W
+// rows sit in LDS with their 16-byte chunks XOR-swizzled by (row / 2) % 8. Those 8-byte
+// reads of 16 rows still meet 2-way bank conflicts (the copies move 16-byte chunks, so
+// no swizzle can separate the two 8-byte halves of a chunk): measured on MI355X, 17.8%
+// of the kernel's cycles against 21.8% with row % 8.
+// 32 x 32 tiles: two v_mfma_i32_32x32x16_i8 per block. Lane (row r = lane % 32, half
+// h = lane / 32) feeds K values 16 h + 8 s .. + 7 of the block in step s (A and W alike,
+// so the exact INT32 sums are the block's), i.e. one 16-byte chunk 2 q + h per block:
+// 16-byte reads, chunks swizzled by row % 8, as in the other GEMMs. The scale products
+// of two blocks come from one v_mfma_f32_32x32x1f32 (two 32 x 32 outer products,
+// rounded as the FP32 multiply: checked on MI355X over 4.2 M operand pairs, like the
+// 16 x 16 form), in the layout of the INT32 output: register 16 b + i holds block b's
+// row 8 (i / 4) + 4 h + i % 4, column lane % 32 (checked on MI355X).
 template <class T>
 __global__ void __launch_bounds__(T::kThreads, T::kOcc) q8_ring_kernel(
     const int8_t* __restrict__ a, const float* __restrict__ sa, const int8_t* __restrict__ w,
@@ -359,7 +373,7 @@ __global__ void __launch_bounds__(T::kThreads, T::kOcc) q8_ring_kernel(
       const bool is_a = j < T::nA;
       const int jj = is_a ? j : j - T::nA;
       const int r = jj * 8 + (lane >> 3);
-      const int chunk = (lane & 7) ^ ((r >> 1) & 7);
+      const int chunk = (lane & 7) ^ (T::kMfma32 ? (r & 7) : ((r >> 1) & 7));
       const int first = is_a ? row0 : col0;
       c_rsrc[i] = is_a ? a_rsrc : w_rsrc;
       c_lds[i] = (is_a ? 0 : T::kA) + jj * 1024;
@@ -408,14 +422,9 @@ __global__ void __launch_bounds__(T::kThreads, T::kOcc) q8_ring_kernel(
   };
 
   const int wm = wave % T::kWM, wn = wave / T::kWM;
-  const int lr = lane & 15, lq = lane >> 4;
-  float sum[T::kTM][T::kTN][4];
+  float sum[T::kTM * T::kTN * 4];
 #pragma unroll
-  for (int ti = 0; ti < T::kTM; ++ti)
-#pragma unroll
-    for (int tj = 0; tj < T::kTN; ++tj)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sum[ti][tj][i] = 0.f;
+  for (int i = 0; i < T::kTM * T::kTN * 4; ++i) sum[i] = 0.f;
 
 #pragma unroll
   for (int st = 0; st < T::kNS - 1; ++st) issue(st);
@@ -429,68 +438,111 @@ __global__ void __launch_bounds__(T::kThreads, T::kOcc) q8_ring_kernel(
     issue(t + T::kNS - 1);
     __builtin_amdgcn_sched_barrier(0);
     const auto* base = lds + (t % T::kNS) * T::kStage;
-    f32x16_t scl[T::kTM][T::kTN];
-    {
-      float sa_op[T::kTM], sw_op[T::kTN];
+    if constexpr (T::kMfma32) {
+      const int lr = lane & 31, lh = lane >> 5;
+      const int arow = wm * 32 + lr, wrow = wn * 32 + lr;
 #pragma unroll
-      for (int ti = 0; ti < T::kTM; ++ti) {
-        const int row = (wm * T::kTM + ti) * 16 + lr;
-        sa_op[ti] = *reinterpret_cast<const __attribute__((address_space(3))) float*>(
-            base + T::kA + T::kW + row * 16 + lq * 4);
+      for (int p = 0; p < 2; ++p) {  // blocks 2p and 2p + 1
+        const float sa_op = *reinterpret_cast<const __attribute__((address_space(3))) float*>(
+            base + T::kA + T::kW + arow * 16 + (2 * p + lh) * 4);
+        const float sw_op = half_to_float(*reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(
+            base + T::kA + T::kW + T::kSa + p * (T::kBN * 4) + wrow * 4 + lh * 2));
+        const f32x32_t scl = __builtin_amdgcn_mfma_f32_32x32x1f32(sa_op, sw_op, f32x32_t{}, 0, 0, 0);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const int chunk = 2 * (2 * p + b) + lh;
+          const u32x4 af = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+              base + arow * 128 + ((chunk ^ (arow & 7)) * 16));
+          const u32x4 wf = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+              base + T::kA + wrow * 128 + ((chunk ^ (wrow & 7)) * 16));
+          i32x16_t acc = {};
+#pragma unroll
+          for (int st2 = 0; st2 < 2; ++st2)
+            acc = __builtin_amdgcn_mfma_i32_32x32x16_i8(
+                int64_t(af[2 * st2]) | (int64_t(af[2 * st2 + 1]) << 32),
+                int64_t(wf[2 * st2]) | (int64_t(wf[2 * st2 + 1]) << 32), acc, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sum[i] = __builtin_fmaf(float(acc[i]), scl[16 * b + i], sum[i]);
+        }
       }
+    } else {
+      const int lr = lane & 15, lq = lane >> 4;
+      f32x16_t scl[T::kTM][T::kTN];
+      {
+        float sa_op[T::kTM], sw_op[T::kTN];
 #pragma unroll
-      for (int tj = 0; tj < T::kTN; ++tj) {
-        const int col = (wn * T::kTN + tj) * 16 + lr;
-        sw_op[tj] = half_to_float(*reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(
-            base + T::kA + T::kW + T::kSa + (lq >> 1) * (T::kBN * 4) + col * 4 + (lq & 1) * 2));
-      }
-#pragma unroll
-      for (int ti = 0; ti < T::kTM; ++ti)
-#pragma unroll
-        for (int tj = 0; tj < T::kTN; ++tj)
-          scl[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x1f32(sa_op[ti], sw_op[tj], f32x16_t{}, 0, 0, 0);
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      // Lane group lq takes bytes 8 lq .. 8 lq + 7 of block q: chunk 2q + lq / 2.
-      const int chunk = 2 * q + (lq >> 1);
-      int64_t af[T::kTM], wf[T::kTN];
-#pragma unroll
-      for (int ti = 0; ti < T::kTM; ++ti) {
-        const int row = (wm * T::kTM + ti) * 16 + lr;
-        af[ti] = *reinterpret_cast<const __attribute__((address_space(3))) int64_t*>(
-            base + row * 128 + ((chunk ^ ((row >> 1) & 7)) * 16) + (lq & 1) * 8);
-      }
-#pragma unroll
-      for (int tj = 0; tj < T::kTN; ++tj) {
-        const int row = (wn * T::kTN + tj) * 16 + lr;
-        wf[tj] = *reinterpret_cast<const __attribute__((address_space(3))) int64_t*>(
-            base + T::kA + row * 128 + ((chunk ^ ((row >> 1) & 7)) * 16) + (lq & 1) * 8);
-      }
-#pragma unroll
-      for (int ti = 0; ti < T::kTM; ++ti)
+        for (int ti = 0; ti < T::kTM; ++ti) {
+          const int row = (wm * T::kTM + ti) * 16 + lr;
+          sa_op[ti] = *reinterpret_cast<const __attribute__((address_space(3))) float*>(
+              base + T::kA + T::kW + row * 16 + lq * 4);
+        }
 #pragma unroll
         for (int tj = 0; tj < T::kTN; ++tj) {
-          const i32x4_t acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[ti], wf[tj],
-                                                                   i32x4_t{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            sum[ti][tj][i] = __builtin_fmaf(float(acc[i]), scl[ti][tj][4 * q + i], sum[ti][tj][i]);
+          const int col = (wn * T::kTN + tj) * 16 + lr;
+          sw_op[tj] = half_to_float(*reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(
+              base + T::kA + T::kW + T::kSa + (lq >> 1) * (T::kBN * 4) + col * 4 + (lq & 1) * 2));
         }
+#pragma unroll
+        for (int ti = 0; ti < T::kTM; ++ti)
+#pragma unroll
+          for (int tj = 0; tj < T::kTN; ++tj)
+            scl[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x1f32(sa_op[ti], sw_op[tj], f32x16_t{}, 0, 0, 0);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        // Lane group lq takes bytes 8 lq .. 8 lq + 7 of block q: chunk 2q + lq / 2.
+        const int chunk = 2 * q + (lq >> 1);
+        int64_t af[T::kTM], wf[T::kTN];
+#pragma unroll
+        for (int ti = 0; ti < T::kTM; ++ti) {
+          const int row = (wm * T::kTM + ti) * 16 + lr;
+          af[ti] = *reinterpret_cast<const __attribute__((address_space(3))) int64_t*>(
+              base + row * 128 + ((chunk ^ ((row >> 1) & 7)) * 16) + (lq & 1) * 8);
+        }
+#pragma unroll
+        for (int tj = 0; tj < T::kTN; ++tj) {
+          const int row = (wn * T::kTN + tj) * 16 + lr;
+          wf[tj] = *reinterpret_cast<const __attribute__((address_space(3))) int64_t*>(
+              base + T::kA + row * 128 + ((chunk ^ ((row >> 1) & 7)) * 16) + (lq & 1) * 8);
+        }
+#pragma unroll
+        for (int ti = 0; ti < T::kTM; ++ti)
+#pragma unroll
+          for (int tj = 0; tj < T::kTN; ++tj) {
+            const i32x4_t acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[ti], wf[tj],
+                                                                     i32x4_t{0, 0, 0, 0}, 0, 0, 0);
+            float* o = sum + (ti * T::kTN + tj) * 4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              o[i] = __builtin_fmaf(float(acc[i]), scl[ti][tj][4 * q + i], o[i]);
+          }
+      }
     }
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // drain the trailing (out-of-range) copies
+  if constexpr (T::kMfma32) {
+    const int lr = lane & 31, lh = lane >> 5;
+    const int col = col0 + wn * 32 + lr;
 #pragma unroll
-  for (int ti = 0; ti < T::kTM; ++ti)
-#pragma unroll
-    for (int tj = 0; tj < T::kTN; ++tj) {
-      const int col = col0 + (wn * T::kTN + tj) * 16 + lr;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = row0 + (wm * T::kTM + ti) * 16 + lq * 4 + i;
-        if (row < m && col < n) y[int64_t(row) * n + col] = uint16_t(f32_to_bf16(sum[ti][tj][i]));
-      }
+    for (int i = 0; i < 16; ++i) {
+      const int row = row0 + wm * 32 + 8 * (i / 4) + 4 * lh + (i % 4);
+      if (row < m && col < n) y[int64_t(row) * n + col] = uint16_t(f32_to_bf16(sum[i]));
     }
+  } else {
+    const int lr = lane & 15, lq = lane >> 4;
+#pragma unroll
+    for (int ti = 0; ti < T::kTM; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < T::kTN; ++tj) {
+        const int col = col0 + (wn * T::kTN + tj) * 16 + lr;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = row0 + (wm * T::kTM + ti) * 16 + lq * 4 + i;
+          if (row < m && col < n)
+            y[int64_t(row) * n + col] = uint16_t(f32_to_bf16(sum[(ti * T::kTN + tj) * 4 + i]));
+        }
+      }
+  }
 }
 
 template <class T>
@@ -506,8 +558,8 @@ hipError_t launch_ring(const int8_t* a, const float* sa, const int8_t* w, const 
   return hipGetLastError();
 }
 
-using Ring64 = RingTile<2, 4, 2, 1, 4, 2>;   // 64 x 64, waves of 32 x 16, two per CU
-using Ring128 = RingTile<4, 4, 2, 2, 4, 4>;  // 128 x 128 on 16 waves, one per CU
+using Ring64 = RingTile<2, 4, 2, 1, 4, 2>;         // 64 x 64, waves of 32 x 16, two per CU
+using Ring128 = RingTile<4, 4, 2, 2, 4, 4, true>;  // 128 x 128, 16 waves of 32 x 32, one per CU
 
 }  // namespace
 
@@ -534,8 +586,10 @@ hipError_t launch_q8_block_mm(const int8_t* a, const float* sa, const int8_t* w,
   const auto* s16 = static_cast<const uint16_t*>(sw);
   auto* out = static_cast<uint16_t*>(y);
   if (k % 128 == 0 && reinterpret_cast<uintptr_t>(sw) % 4 == 0) {
-    // The ring kernel; 128 x 128 tiles once there are two per CU (M = N = K = 4096: 257
-    // against 272 us for 64 x 64), else 64 x 64.
+    // The ring kernel; 128 x 128 tiles on 32 x 32 MFMAs once there are two per CU
+    // (M = N = K = 4096: 228 us, against 246 us for 16 x 16 MFMAs and 272 us for 64 x 64
+    // tiles), else 64 x 64 on 16 x 16 MFMAs (at M = 2048, N = 1024, K = 4096 the 32 x 32
+    // form of any of three tile shapes is no faster).
     const int cus = device_cu_count();
     const int64_t tiles128 = int64_t((m + 127) / 128) * ((n + 127) / 128);
     if (cus > 0 && tiles128 >= 2 * int64_t(cus))
