@@ -293,7 +293,11 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
     barrier_fenced();                  // every wave is past its last fragment reads
 
     // The next tile's first copies go out now, into A slot 0 and W slots 0 and 1, and
-    // land while this tile's results are stored through A slot 1.
+    // land while this tile's results are stored through A slot 1. Every load of this
+    // tile has landed by now (each wave waited for its last copies); the explicit wait
+    // says so to the compiler, which otherwise waits for those first copies before the
+    // epilogue's first use of the scales loaded at the tile start.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     const int tile_m0 = m0, tile_n0 = n0;
     const bool more = r + 1 < my_tiles;
     if (more) {
