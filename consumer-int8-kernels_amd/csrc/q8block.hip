@@ -580,9 +580,6 @@ hipError_t launch_quantize_block32(const void* x, int8_t* a, float* sa, int m, i
 hipError_t launch_q8_block_mm(const int8_t* a, const float* sa, const int8_t* w,
                               const void* sw, void* y, int m, int n, int k,
                               hipStream_t stream) {
-  // 64 x 64 tiles on 8 waves (each 16 rows x 32 columns), K steps of 256; 32 x 32 tiles on
-  // 4 waves when the larger tiles would leave CUs idle (tile-shape sweep at N = 1024,
-  // K = 4096, M = 512 and 2048).
   const auto* s16 = static_cast<const uint16_t*>(sw);
   auto* out = static_cast<uint16_t*>(y);
   if (k % 128 == 0 && reinterpret_cast<uintptr_t>(sw) % 4 == 0) {
@@ -596,6 +593,9 @@ hipError_t launch_q8_block_mm(const int8_t* a, const float* sa, const int8_t* w,
       return launch_ring<Ring128>(a, sa, w, s16, out, m, n, k, stream);
     return launch_ring<Ring64>(a, sa, w, s16, out, m, n, k, stream);
   }
+  // Other K or 2-byte-aligned sw: the step kernel, 64 x 64 tiles on 8 waves (each 16 rows
+  // x 32 columns), K steps of 256; 32 x 32 tiles on 4 waves when the larger tiles would
+  // leave CUs idle (tile-shape sweep at N = 1024, K = 4096, M = 512 and 2048).
   const int64_t big_tiles = int64_t((m + 63) / 64) * ((n + 63) / 64);
   if (big_tiles >= 256)
     launch_q8_tile<4, 2, 1, 2, 256, 4, 2>(a, sa, w, s16, out, m, n, k, stream);
