@@ -83,7 +83,10 @@ struct PPConfig {
   static constexpr int kEpiRowBytes = (BN / 2) * 2 + 16;
   static constexpr int kEpiPassBytes = 16 * kEpiRowBytes;  // one 16-row block per wave
   static constexpr int kLdsBytes = kRingBytes;
-  static constexpr int GROUP_M = 8;
+  // m tiles per raster group: each XCD's 32 tiles of a round then cover 4 m x 8 n
+  // tiles (measured on MI355X against 2, 8 and 16: configs[2] 277-278 against 280-286
+  // us at 8; configs[3] 1,108-1,110 against 1,152-1,154 us).
+  static constexpr int GROUP_M = 4;
   static_assert(kCopies * WM == kABlocks && (kCopies - 1) * WM == kWBlocks, "copies");
   static_assert(3 * (kCopies - 1) < 2 * (TM + TN), "copies fit between the fragment reads");
   static_assert(kLdsBytes <= 160 * 1024, "LDS");
