@@ -225,10 +225,12 @@ __global__ void __launch_bounds__(C::kThreads) gguf_q8_span_kernel(
   const int lane = threadIdx.x & 63;
   const int range = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row = lane & 15, q = lane >> 4;
+  // K is walked in chunks of kS * kSpb blocks of 64 (one chunk unless K > 8192 with
+  // kSpb = 8); each chunk splits its blocks into kS ranges, one per wave.
   const int kblocks = k / 64;
-  const int range_len = (kblocks + C::kS - 1) / C::kS;  // <= kSpb (host-checked)
-  const int kb_first = range * range_len;
-  const int my_slots = max(0, min(kb_first + range_len, kblocks) - kb_first);
+  constexpr int kChunkBlocks = C::kS * C::kSpb;
+  const int nchunks = (kblocks + kChunkBlocks - 1) / kChunkBlocks;
+  int kb_first = 0, my_slots = 0;
 
   // Group g's codes [n, k] and scales [n, k / 32]; x rows of group g at stride xs.
   const int8_t* gcodes = codes + int64_t(g) * n * k;
@@ -253,28 +255,6 @@ __global__ void __launch_bounds__(C::kThreads) gguf_q8_span_kernel(
                : kOutOfRange;
   };
 
-  // x fragments: lane (row, q) holds x[row, g, kb * 64 + 16 q + 8 h + 0..7].
-  u32x4 xf[C::kSpb][2];
-#pragma unroll
-  for (int s = 0; s < C::kSpb; ++s) {
-    const bool valid = row < m && s < my_slots;
-    const uint32_t base =
-        uint32_t((int64_t(row) * xs + (kb_first + s) * 64 + q * 16) * 2);
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      xf[s][h] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, valid ? base + 16u * h : kOutOfRange,
-                                                       0, 0));
-  }
-  u32x4 wv[C::kSpb];
-  uint32_t sv[C::kSpb];
-#pragma unroll
-  for (int s = 0; s < C::kSpb; ++s) {
-    wv[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(0, s), 0, 0));
-    sv[s] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, s_offset(0, s), 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
   // Adds the partials of local blocks [lb0, lb0 + count) in range order and stores them.
   auto reduce = [&](int lb0, int count) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
@@ -294,29 +274,69 @@ __global__ void __launch_bounds__(C::kThreads) gguf_q8_span_kernel(
     workgroup_barrier();
   };
 
-  for (int lb = 0; lb < nlocal; ++lb) {
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int chunk = 0; chunk < nchunks; ++chunk) {  // uniform over the workgroup
+    const int cb0 = chunk * kChunkBlocks;
+    const int cblocks = min(kblocks - cb0, kChunkBlocks);
+    const int range_len = (cblocks + C::kS - 1) / C::kS;  // <= kSpb
+    kb_first = cb0 + range * range_len;
+    my_slots = max(0, min(kb_first + range_len, cb0 + cblocks) - kb_first);
+
+    // x fragments: lane (row, q) holds x[row, g, kb * 64 + 16 q + 8 h + 0..7].
+    u32x4 xf[C::kSpb][2];
 #pragma unroll
     for (int s = 0; s < C::kSpb; ++s) {
-      waitcnt<vmcnt_imm(2 * C::kSpb - 2)>();  // W(lb, s) and its scale have landed
-      if (s < my_slots) {
-        const float sc = f16_to_f32(sv[s]);
-        const u32x4 wq = wv[s];
-        const u32x2 d0 = dequant4(wq[0], sc), d1 = dequant4(wq[1], sc);
-        const u32x2 d2 = dequant4(wq[2], sc), d3 = dequant4(wq[3], sc);
-        acc = mfma_bf16(u32x4{d0[0], d0[1], d1[0], d1[1]}, xf[s][0], acc);
-        acc = mfma_bf16(u32x4{d2[0], d2[1], d3[0], d3[1]}, xf[s][1], acc);
-      }
-      wv[s] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(lb + 1, s), 0, 0));
-      sv[s] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, s_offset(lb + 1, s), 0, 0);
+      const bool valid = row < m && s < my_slots;
+      const uint32_t base =
+          uint32_t((int64_t(row) * xs + (kb_first + s) * 64 + q * 16) * 2);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        xf[s][h] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, valid ? base + 16u * h : kOutOfRange,
+                                                         0, 0));
+    }
+    u32x4 wv[C::kSpb];
+    uint32_t sv[C::kSpb];
+#pragma unroll
+    for (int s = 0; s < C::kSpb; ++s) {
+      wv[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(0, s), 0, 0));
+      sv[s] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, s_offset(0, s), 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
-    partial[lb % C::kBatch][range][lane] = acc;
-    if (lb % C::kBatch == C::kBatch - 1 || lb + 1 == nlocal)  // uniform
-      reduce(lb / C::kBatch * C::kBatch, lb % C::kBatch + 1);
+
+    for (int lb = 0; lb < nlocal; ++lb) {
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < C::kSpb; ++s) {
+        waitcnt<vmcnt_imm(2 * C::kSpb - 2)>();  // W(lb, s) and its scale have landed
+        if (s < my_slots) {
+          const float sc = f16_to_f32(sv[s]);
+          const u32x4 wq = wv[s];
+          const u32x2 d0 = dequant4(wq[0], sc), d1 = dequant4(wq[1], sc);
+          const u32x2 d2 = dequant4(wq[2], sc), d3 = dequant4(wq[3], sc);
+          acc = mfma_bf16(u32x4{d0[0], d0[1], d1[0], d1[1]}, xf[s][0], acc);
+          acc = mfma_bf16(u32x4{d2[0], d2[1], d3[0], d3[1]}, xf[s][1], acc);
+        }
+        wv[s] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(lb + 1, s), 0, 0));
+        sv[s] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, s_offset(lb + 1, s), 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (nchunks == 1) {
+        partial[lb % C::kBatch][range][lane] = acc;
+        if (lb % C::kBatch == C::kBatch - 1 || lb + 1 == nlocal)  // uniform
+          reduce(lb / C::kBatch * C::kBatch, lb % C::kBatch + 1);
+      } else {
+        // Several chunks: every local block keeps its slot (nlocal <= kBatch, host-checked)
+        // and sums its chunks' partials in chunk order.
+        if (chunk == 0)
+          partial[lb][range][lane] = acc;
+        else
+          partial[lb][range][lane] += acc;
+      }
+    }
+    waitcnt<vmcnt_imm(0)>();  // drain the trailing (out-of-range) loads of the chunk
   }
-  waitcnt<vmcnt_imm(0)>();  // drain the trailing (out-of-range) loads before exit
+  if (nchunks > 1) reduce(0, nlocal);
 }
 
 template <class C>
@@ -589,8 +609,12 @@ hipError_t launch_gguf_q8_packed_mm(const void* x, const int8_t* codes, const vo
   // in registers (K <= 16 ranges x 8 blocks x 64) and x's byte range fits a buffer.
   const int cus = device_cu_count();
   const int range_len = (k / 64 + 15) / 16;
-  if (m <= 16 && cus > 0 && range_len <= 8 && (int64_t(m - 1) * xs + k) * 2 <= INT32_MAX &&
-      int64_t(n) * k <= INT32_MAX) {
+  // K > 8192 runs the span kernel in chunks of 8192 while a workgroup's partial sums of
+  // all its channel blocks fit the LDS at once (span <= 8 blocks of 16).
+  const int per_group = cus > 0 ? max(1, min((cus + groups - 1) / groups, (n + 15) / 16)) : 1;
+  const int span_blocks = ((n + per_group - 1) / per_group + 15) / 16;
+  if (m <= 16 && cus > 0 && (range_len <= 8 || span_blocks <= 8) &&
+      (int64_t(m - 1) * xs + k) * 2 <= INT32_MAX && int64_t(n) * k <= INT32_MAX) {
     if (range_len <= 2)
       return run_span<GgufSpanConfig<2>>(x, codes, scales, out, m, n, k, groups, xs, xg, cus, stream);
     if (range_len <= 4)

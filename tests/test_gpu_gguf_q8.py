@@ -10,8 +10,9 @@ On top of that every output element is held to the oracle (oracle.gguf_q8_packed
 a float64 product of the same BF16 weights): |out - exact| <= one BF16 ulp of the exact
 value + K * 2^-24 * sum_k |x * wq| (any FP32 summation order). Further cases reach
 ragged N (scalar stores), padded row strides, a single K stage, large K, M on both
-sides of the 16-row switch (m <= 16 runs the balanced-span kernel of the W8A16 GEMV
-while K <= 8192), the 256- and 128-row tiles of larger batches (1, 2, 3, 7 and 8 K
+sides of the 16-row switch (m <= 16 runs the balanced-span kernel of the W8A16 GEMV,
+in chunks of 8192 along K beyond that while a workgroup spans at most 8 channel
+blocks), the 256- and 128-row tiles of larger batches (1, 2, 3, 7 and 8 K
 stages), the 64-row tile kernel that takes x beyond a 2 GiB buffer range, extreme codes
 and scales, and guard sentinels around the output.
 """
@@ -94,7 +95,10 @@ CASES = [
     (17, 1, 1000, 5120, 0),     # smallest M past the span kernel, ragged N
     (200, 2, 130, 1536, 64),    # ragged M and N (N % 4 == 2: scalar stores), padded rows
     (64, 4, 96, 64, 8),         # one K stage
-    (5, 2, 37, 16384, 0),       # long K: the tile kernel at m <= 16
+    (5, 2, 37, 16384, 0),       # long K at m <= 16: the span kernel in two K chunks
+    (8, 1, 4096, 14336, 0),     # span kernel, K chunks of 128 and 96 blocks of 64
+    (3, 2, 300, 9216, 64),      # span kernel, a last K chunk of one block per wave
+    (2, 1, 33280, 9216, 0),     # K > 8192 with 9 channel blocks per CU: the tile kernel
     (256, 1, 512, 2048, 0),
     (7, 3, 300, 2048, 64),      # m <= 16 span kernel: groups, padded rows, ragged spans
     (16, 2, 4100, 8192, 0),     # span kernel at its longest K, more channels than CUs x 16
