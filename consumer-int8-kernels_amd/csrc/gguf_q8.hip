@@ -339,13 +339,18 @@ __global__ void __launch_bounds__(C::kThreads) gguf_q8_span_kernel(
   if (nchunks > 1) reduce(0, nlocal);
 }
 
+// Channels per span-kernel workgroup: about one workgroup per CU over all groups, each
+// over at least 16 channels.
+int span_channels(int n, int groups, int cus) {
+  const int per_group = max(1, min((cus + groups - 1) / groups, (n + 15) / 16));
+  return (n + per_group - 1) / per_group;
+}
+
 template <class C>
 hipError_t run_span(const void* x, const int8_t* codes, const void* scales, void* out, int m,
                     int n, int k, int groups, int64_t xs, int64_t xg, int cus,
                     hipStream_t stream) {
-  // About one workgroup per CU over all groups, each over at least 16 channels.
-  const int per_group = max(1, min((cus + groups - 1) / groups, (n + 15) / 16));
-  const int span = (n + per_group - 1) / per_group;
+  const int span = span_channels(n, groups, cus);
   const dim3 grid(unsigned((n + span - 1) / span), unsigned(groups));
   gguf_q8_span_kernel<C><<<grid, C::kThreads, 0, stream>>>(
       static_cast<const uint16_t*>(x), codes, static_cast<const uint16_t*>(scales),
@@ -611,8 +616,7 @@ hipError_t launch_gguf_q8_packed_mm(const void* x, const int8_t* codes, const vo
   const int range_len = (k / 64 + 15) / 16;
   // K > 8192 runs the span kernel in chunks of 8192 while a workgroup's partial sums of
   // all its channel blocks fit the LDS at once (span <= 8 blocks of 16).
-  const int per_group = cus > 0 ? max(1, min((cus + groups - 1) / groups, (n + 15) / 16)) : 1;
-  const int span_blocks = ((n + per_group - 1) / per_group + 15) / 16;
+  const int span_blocks = cus > 0 ? (span_channels(n, groups, cus) + 15) / 16 : 0;
   if (m <= 16 && cus > 0 && (range_len <= 8 || span_blocks <= 8) &&
       (int64_t(m - 1) * xs + k) * 2 <= INT32_MAX && int64_t(n) * k <= INT32_MAX) {
     if (range_len <= 2)
