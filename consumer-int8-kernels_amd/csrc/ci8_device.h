@@ -82,6 +82,22 @@ __device__ __forceinline__ u32x2 codes8(const u32x4& packed, float scale, float 
   return out;
 }
 
+// Inputs larger than MI355X's 256 MB Infinity Cache (MALL) cannot stay cached between
+// the kernels that write and read them; the streaming kernels read those with
+// nontemporal loads (measured: quantize_rows [16384, 17408] 155 -> 138 us, silu_mul
+// [16384, 2 x 17408] 285 -> 261 us; at [4096, 5120], where the input fits, nontemporal
+// loads were 6% slower).
+constexpr int64_t kMallBytes = int64_t(256) << 20;
+
+// One 16-byte load, nontemporal when kNt.
+template <bool kNt>
+__device__ __forceinline__ u32x4 load16(const void* p) {
+  if constexpr (kNt)
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  else
+    return *reinterpret_cast<const u32x4*>(p);
+}
+
 // Raw buffer resource over `bytes` bytes starting at `base`. Loads at byte offsets
 // >= bytes return zero, which covers row and column tails without branches.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {

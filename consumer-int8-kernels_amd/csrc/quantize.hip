@@ -31,7 +31,7 @@ __device__ __forceinline__ float wave_max(float v) {
 // Vector path. Requires k % 8 == 0, x 16-byte aligned, codes 8-byte aligned.
 // kWaves waves cooperate on one row when kWaves > 1 (very wide rows).
 // Grouped: output row o reads input row (o % m) * groups + o / m ([m,g,k] -> [g,m,k]).
-template <int kPacks, int kWaves, bool kGrouped>
+template <int kPacks, int kWaves, bool kGrouped, bool kNt>
 __global__ void __launch_bounds__(256) quantize_rows_vec_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ codes, float* __restrict__ scales,
     int rows, int k, int m, int groups) {
@@ -51,7 +51,7 @@ __global__ void __launch_bounds__(256) quantize_rows_vec_kernel(
   for (int i = 0; i < kPacks; ++i) {
     const int col = ((i * kWaves + part) * kWave + lane) * 8;
     packed[i] = u32x4{0, 0, 0, 0};
-    if (active && col < k) packed[i] = *reinterpret_cast<const u32x4*>(src + col);
+    if (active && col < k) packed[i] = load16<kNt>(src + col);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t word = packed[i][j];
@@ -109,11 +109,17 @@ hipError_t dispatch(const void* x, int8_t* codes, float* scales, int rows, int k
   const bool vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
                    (reinterpret_cast<uintptr_t>(codes) % 8 == 0) && (k % 8 == 0);
   const int packs = (k + 511) / 512;  // 16-byte packs per lane with one wave per row
+  // Inputs past the MALL's size are read with nontemporal loads (kMallBytes).
+  const bool nt = int64_t(rows) * k * 2 > kMallBytes;
 #define CI8_QW(W, P)                                                                       \
   if (packs <= (W) * (P)) {                                                                \
-    quantize_rows_vec_kernel<P, W, kGrouped><<<(rows + 4 / (W) - 1) / (4 / (W)), 256, 0,     \
-                                               stream>>>(src, codes, scales, rows, k, m,   \
-                                                         groups);                          \
+    const int blocks = (rows + 4 / (W) - 1) / (4 / (W));                                   \
+    if (nt)                                                                                \
+      quantize_rows_vec_kernel<P, W, kGrouped, true><<<blocks, 256, 0, stream>>>(           \
+          src, codes, scales, rows, k, m, groups);                                         \
+    else                                                                                   \
+      quantize_rows_vec_kernel<P, W, kGrouped, false><<<blocks, 256, 0, stream>>>(          \
+          src, codes, scales, rows, k, m, groups);                                         \
     return hipGetLastError();                                                              \
   }
   // Waves per row: four once a row has four packs, so each lane holds at most a few

@@ -146,14 +146,14 @@ __global__ void __launch_bounds__(64 * kWaves) silu_mul_quantize_kernel(
 
 // Elementwise SwiGLU, eight outputs per lane; blockIdx.y is the row. Requires
 // k % 8 == 0 and 16-byte aligned x and out.
+template <bool kNt>
 __global__ void __launch_bounds__(256) silu_mul_kernel(const uint16_t* __restrict__ x,
                                                        uint16_t* __restrict__ out, int k) {
   const int col = (blockIdx.x * 256 + threadIdx.x) * 8;
   if (col >= k) return;
   const int64_t row = blockIdx.y;
   const uint16_t* gate = x + row * 2 * k + col;
-  const u32x4 v = swiglu8(*reinterpret_cast<const u32x4*>(gate),
-                          *reinterpret_cast<const u32x4*>(gate + k));
+  const u32x4 v = swiglu8(load16<kNt>(gate), load16<kNt>(gate + k));
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(out + row * k + col));
 }
 
@@ -193,7 +193,12 @@ hipError_t launch_silu_mul(const void* x, void* out, int m, int k, hipStream_t s
   const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(out) % 16 == 0 && k % 8 == 0;
   if (vec) {
-    silu_mul_kernel<<<dim3((k / 8 + 255) / 256, m), 256, 0, stream>>>(src, dst, k);
+    // Inputs past the MALL's size are read with nontemporal loads (kMallBytes).
+    const dim3 grid((k / 8 + 255) / 256, m);
+    if (count * 4 > kMallBytes)
+      silu_mul_kernel<true><<<grid, 256, 0, stream>>>(src, dst, k);
+    else
+      silu_mul_kernel<false><<<grid, 256, 0, stream>>>(src, dst, k);
   } else {
     silu_mul_scalar_kernel<<<int((count + 255) / 256), 256, 0, stream>>>(src, dst, m, k);
   }
