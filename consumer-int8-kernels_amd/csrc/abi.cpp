@@ -135,8 +135,14 @@ int ci8_cutlass_channel_mm_noalloc(const int8_t* a, const int8_t* w, const float
   if (!aligned(a, 16) || !aligned(w, 16) || !aligned(a_scale, 4) || !aligned(w_scale, 2) ||
       !aligned(out, 2))
     return fail(CI8_ERR_ALIGNMENT, "cutlass_channel_mm requires aligned buffers");
-  return launched(ci8::launch_cutlass_channel_mm_noalloc(a, w, a_scale, w_scale, out, int(m),
-                                                         int(n), int(k), as_stream(stream)));
+  const hipError_t e = ci8::launch_cutlass_channel_mm_noalloc(a, w, a_scale, w_scale, out,
+                                                              int(m), int(n), int(k),
+                                                              as_stream(stream));
+  if (e == hipErrorStreamCaptureUnsupported)
+    return fail(CI8_ERR_LAUNCH,
+                "cutlass_channel_mm_noalloc: the first call on a device must run outside "
+                "graph capture (it looks up the device's scratch address)");
+  return launched(e);
 }
 
 int ci8_channel_mm(const int8_t* a, const uint8_t* w_u8, const float* a_scale,

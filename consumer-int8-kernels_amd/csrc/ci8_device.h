@@ -6,6 +6,8 @@
 
 #include <atomic>
 
+#include "lds_budget.h"
+
 namespace ci8 {
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
@@ -106,15 +108,42 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 // An offset past every valid buffer (buffers are limited to INT_MAX bytes).
 constexpr uint32_t kOutOfRange = 0x80000000u;
 
-// Raises `kernel`'s dynamic LDS limit to `bytes` on the first call that succeeds. The
-// attribute is idempotent, so concurrent first calls may both set it; the flag is atomic.
-template <class Kernel>
-inline hipError_t raise_lds_limit_once(Kernel kernel, int bytes, std::atomic<bool>& done) {
-  if (done.load(std::memory_order_acquire)) return hipSuccess;
-  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  if (e == hipSuccess) done.store(true, std::memory_order_release);
-  return e;
+// A kernel as a type, for launch helpers that take several kernels of one signature.
+template <auto Kernel>
+struct kernel_constant {
+  static constexpr auto value = Kernel;
+};
+
+// Every launch that requests dynamic LDS calls prepare_lds<kernel>(bytes) first, with the
+// bytes it requests. It returns hipErrorInvalidConfiguration (and the caller launches
+// nothing) when the kernel's static LDS plus those bytes exceed the 160 KiB a workgroup
+// can hold; otherwise, on the first launch of that kernel that needs more than the default
+// 64 KiB, it raises the kernel's dynamic-LDS attribute to the rest of the budget. The
+// kernel's static LDS is looked up once. State is kept per kernel (per template
+// argument); concurrent first calls may both query or set the idempotent attributes.
+template <auto Kernel>
+inline hipError_t prepare_lds(int64_t dynamic_bytes) {
+  static std::atomic<int64_t> static_bytes_cache{-1};
+  static std::atomic<bool> raised{false};
+  int64_t static_bytes = static_bytes_cache.load(std::memory_order_acquire);
+  if (static_bytes < 0) {
+    hipFuncAttributes attributes{};
+    if (const hipError_t e =
+            hipFuncGetAttributes(&attributes, reinterpret_cast<const void*>(Kernel));
+        e != hipSuccess)
+      return e;
+    static_bytes = int64_t(attributes.sharedSizeBytes);
+    static_bytes_cache.store(static_bytes, std::memory_order_release);
+  }
+  if (!lds_fits(static_bytes, dynamic_bytes)) return hipErrorInvalidConfiguration;
+  if (dynamic_bytes > kDefaultDynamicLds && !raised.load(std::memory_order_acquire)) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(Kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             int(dynamic_lds_limit(static_bytes)));
+    if (e != hipSuccess) return e;
+    raised.store(true, std::memory_order_release);
+  }
+  return hipSuccess;
 }
 
 // s_waitcnt immediate that waits until at most `n` vector-memory operations are

@@ -331,8 +331,7 @@ template <class C, WeightCode kCode, bool kWorkspace>
 hipError_t run(const int8_t* a, const void* w, const float* sa, const void* sw, void* out,
                int32_t* ws, int m, int n, int k, hipStream_t stream) {
   auto kernel = channel_gemm_kernel<C, kCode, kWorkspace>;
-  static std::atomic<bool> configured{false};
-  if (const hipError_t e = raise_lds_limit_once(kernel, C::kLdsBytes, configured); e != hipSuccess)
+  if (const hipError_t e = prepare_lds<channel_gemm_kernel<C, kCode, kWorkspace>>(C::kLdsBytes); e != hipSuccess)
     return e;
   const int blocks = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
   const bool vec_n = n % 4 == 0 && reinterpret_cast<uintptr_t>(sw) % 8 == 0 &&
@@ -1176,8 +1175,7 @@ template <class C, WeightCode kCode, bool kWorkspace, bool kExactK>
 hipError_t run_wlds_exact(const int8_t* a, const void* w, const float* sa, const void* sw,
                           void* out, int32_t* ws, int m, int n, int k, hipStream_t stream) {
   auto kernel = channel_gemm_wlds_kernel<C, kCode, kWorkspace, kExactK>;
-  static std::atomic<bool> configured{false};
-  if (const hipError_t e = raise_lds_limit_once(kernel, C::kLdsBytes, configured); e != hipSuccess)
+  if (const hipError_t e = prepare_lds<channel_gemm_wlds_kernel<C, kCode, kWorkspace, kExactK>>(C::kLdsBytes); e != hipSuccess)
     return e;
   const int blocks = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
   const bool vec_n = n % 4 == 0 && reinterpret_cast<uintptr_t>(sw) % 8 == 0 &&
@@ -1201,8 +1199,7 @@ template <class C, WeightCode kCode, bool kWorkspace, bool kExactK>
 hipError_t run_k128_exact(const int8_t* a, const void* w, const float* sa, const void* sw,
                           void* out, int32_t* ws, int m, int n, int k, hipStream_t stream) {
   auto kernel = channel_gemm_k128_kernel<C, kCode, kWorkspace, kExactK>;
-  static std::atomic<bool> configured{false};
-  if (const hipError_t e = raise_lds_limit_once(kernel, C::kLdsBytes, configured); e != hipSuccess)
+  if (const hipError_t e = prepare_lds<channel_gemm_k128_kernel<C, kCode, kWorkspace, kExactK>>(C::kLdsBytes); e != hipSuccess)
     return e;
   const int blocks = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
   const bool vec_n = n % 4 == 0 && reinterpret_cast<uintptr_t>(sw) % 8 == 0 &&
@@ -1410,8 +1407,7 @@ template <class C>
 hipError_t run_grouped(const int8_t* a, const int8_t* w, const float* sa, const void* sw,
                        void* out, int groups, int m, int n, int k, hipStream_t stream) {
   auto kernel = grouped_summed_kernel<C>;
-  static std::atomic<bool> configured{false};
-  if (const hipError_t e = raise_lds_limit_once(kernel, C::kLdsBytes, configured); e != hipSuccess)
+  if (const hipError_t e = prepare_lds<grouped_summed_kernel<C>>(C::kLdsBytes); e != hipSuccess)
     return e;
   const int blocks = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
   const bool vec_n = n % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0;
@@ -1455,8 +1451,14 @@ hipError_t launch_grouped_summed_gemm(const int8_t* a, const int8_t* w, const fl
                                       const void* sw, void* out, int groups, int m, int n,
                                       int k, hipStream_t stream) {
   if (m <= 32) return run_grouped<Small>(a, w, sa, sw, out, groups, m, n, k, stream);
+  // The two-waves-per-SIMD kernel copies the row scales into LDS four rows (16 bytes) at a
+  // time at byte offset 4 (g m + row) of a buffer of 4 groups m bytes: that needs m % 4 == 0
+  // and a 16-byte aligned sa (so no copy straddles a group boundary, is misaligned or runs
+  // past the end of sa), and every offset below the 2^31 out-of-range marker.
   if (m >= 1024 && n % 4 == 0 && reinterpret_cast<uintptr_t>(sw) % 8 == 0 &&
-      groups <= grouped_pp_max_groups())
+      groups <= grouped_pp_max_groups() && m % 4 == 0 &&
+      reinterpret_cast<uintptr_t>(sa) % 16 == 0 &&
+      int64_t(groups) * m * 4 < (int64_t(1) << 31))
     return launch_grouped_pp_gemm(a, w, sa, sw, out, groups, m, n, k, stream);
   return run_grouped<Medium>(a, w, sa, sw, out, groups, m, n, k, stream);
 }

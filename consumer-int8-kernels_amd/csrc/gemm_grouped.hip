@@ -350,16 +350,16 @@ hipError_t launch_grouped_pp_gemm(const int8_t* a, const int8_t* w, const float*
   const int blocks = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
   const bool out16 = (reinterpret_cast<uintptr_t>(out) & 15) == 0;
   const int lds = C::kRingBytes + groups * 1024;
-  auto launch = [&](auto kernel) {
-    static std::atomic<bool> configured{false};
-    if (const hipError_t e = raise_lds_limit_once(kernel, 160 * 1024, configured); e != hipSuccess)
-      return e;
+  auto launch = [&](auto kernel_constant) {
+    constexpr auto kernel = decltype(kernel_constant)::value;
+    if (const hipError_t e = prepare_lds<kernel>(lds); e != hipSuccess) return e;
     kernel<<<blocks, C::kThreads, lds, stream>>>(
         a, w, sa, static_cast<const uint16_t*>(sw), static_cast<uint16_t*>(out), groups, m, n, k,
         out16);
     return hipGetLastError();
   };
-  return k % C::BK == 0 ? launch(grouped_pp_kernel<true>) : launch(grouped_pp_kernel<false>);
+  return k % C::BK == 0 ? launch(kernel_constant<grouped_pp_kernel<true>>{})
+                        : launch(kernel_constant<grouped_pp_kernel<false>>{});
 }
 
 }  // namespace ci8

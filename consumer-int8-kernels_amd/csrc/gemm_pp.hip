@@ -377,10 +377,9 @@ hipError_t launch_pp_gemm(const int8_t* a, const void* w, WeightCode code, const
   const int cus = device_cu_count();
   const int grid = cus > 0 && cus < tiles ? cus : tiles;  // one workgroup per CU
   const bool out16 = (reinterpret_cast<uintptr_t>(out) & 15) == 0;
-  auto launch = [&](auto kernel) {
-    static std::atomic<bool> configured{false};
-    if (const hipError_t e = raise_lds_limit_once(kernel, C::kLdsBytes, configured); e != hipSuccess)
-      return e;
+  auto launch = [&](auto kernel_constant) {
+    constexpr auto kernel = decltype(kernel_constant)::value;
+    if (const hipError_t e = prepare_lds<kernel>(C::kLdsBytes); e != hipSuccess) return e;
     kernel<<<grid, C::kThreads, C::kLdsBytes, stream>>>(
         a, static_cast<const int8_t*>(w), sa, static_cast<const uint16_t*>(sw),
         static_cast<uint16_t*>(out), m, n, k, out16);
@@ -388,10 +387,10 @@ hipError_t launch_pp_gemm(const int8_t* a, const void* w, WeightCode code, const
   };
   const bool exact = k % C::BK == 0;
   if (code == WeightCode::kSigned)
-    return exact ? launch(pp_gemm_kernel<true, WeightCode::kSigned>)
-                 : launch(pp_gemm_kernel<false, WeightCode::kSigned>);
-  return exact ? launch(pp_gemm_kernel<true, WeightCode::kBiasedU8>)
-               : launch(pp_gemm_kernel<false, WeightCode::kBiasedU8>);
+    return exact ? launch(kernel_constant<pp_gemm_kernel<true, WeightCode::kSigned>>{})
+                 : launch(kernel_constant<pp_gemm_kernel<false, WeightCode::kSigned>>{});
+  return exact ? launch(kernel_constant<pp_gemm_kernel<true, WeightCode::kBiasedU8>>{})
+               : launch(kernel_constant<pp_gemm_kernel<false, WeightCode::kBiasedU8>>{});
 }
 
 }  // namespace ci8

@@ -249,8 +249,7 @@ template <class C, WeightCode kCode, bool kWorkspace>
 hipError_t run_small(const int8_t* a, const void* w, const float* sa, const void* sw, void* out,
                      int32_t* ws, int m, int n, int k, hipStream_t stream) {
   auto kernel = small_m_gemm_kernel<C, kCode, kWorkspace>;
-  static std::atomic<bool> configured{false};
-  if (const hipError_t e = raise_lds_limit_once(kernel, C::kLdsBytes, configured); e != hipSuccess)
+  if (const hipError_t e = prepare_lds<small_m_gemm_kernel<C, kCode, kWorkspace>>(C::kLdsBytes); e != hipSuccess)
     return e;
   const int blocks = ((m + C::BM - 1) / C::BM) * ((n + C::BN - 1) / C::BN);
   const bool vec_n = n % 4 == 0 && reinterpret_cast<uintptr_t>(sw) % 8 == 0 &&

@@ -767,11 +767,8 @@ hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale
   if (lds <= 64 * 1024) {  // plus 8 KiB of static LDS: two workgroups per CU
     using R = ResidentConfig<8, 10, 8>;
     auto kernel = channel_gemv_resident_kernel<R>;
-    static std::atomic<bool> configured{false};
-    if (lds > 56 * 1024) {
-      if (const hipError_t e = raise_lds_limit_once(kernel, 72 * 1024, configured); e != hipSuccess)
-        return e;
-    }
+    if (const hipError_t e = prepare_lds<channel_gemv_resident_kernel<R>>(lds); e != hipSuccess)
+      return e;
     const int grid = (n + 15) / 16;
     kernel<<<grid, R::kThreads, lds, stream>>>(
         static_cast<const uint16_t*>(x), w, static_cast<const uint16_t*>(scale),
@@ -786,9 +783,7 @@ hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale
   constexpr int kStaticLds = P::kS * 64 * 16;  // partial sums
   if (lds + kStaticLds <= 160 * 1024 && cus > 0) {
     auto kernel = channel_gemv_persistent_kernel<P>;
-    static std::atomic<bool> configured{false};
-    if (const hipError_t e = raise_lds_limit_once(kernel, 160 * 1024 - kStaticLds, configured);
-        e != hipSuccess)
+    if (const hipError_t e = prepare_lds<channel_gemv_persistent_kernel<P>>(lds); e != hipSuccess)
       return e;
     const int grid = min((n + 15) / 16, cus);
     kernel<<<grid, P::kThreads, lds, stream>>>(

@@ -589,9 +589,7 @@ __global__ void __launch_bounds__(C::kThreads, 1) gguf_q8_large_kernel(
 template <class C>
 hipError_t run_large(const void* x, const int8_t* codes, const void* scales, void* out, int m,
                      int n, int k, int groups, int64_t xs, int64_t xg, hipStream_t stream) {
-  static std::atomic<bool> configured{false};
-  if (const hipError_t e = raise_lds_limit_once(gguf_q8_large_kernel<C>, C::kLdsBytes, configured);
-      e != hipSuccess)
+  if (const hipError_t e = prepare_lds<gguf_q8_large_kernel<C>>(C::kLdsBytes); e != hipSuccess)
     return e;
   const int tiles_m = (m + C::BM - 1) / C::BM, tiles_n = (n + C::BN - 1) / C::BN;
   gguf_q8_large_kernel<C><<<unsigned(tiles_m * tiles_n * groups), C::kThreads, C::kLdsBytes, stream>>>(

@@ -11,6 +11,10 @@
 // is a host-side stand-in, not a device address. Each device's address of its own copy
 // is looked up once with hipGetSymbolAddress, with that device current, and cached.
 //
+// The lookup is the one set-up step: the first call on a device must be made outside
+// HIP graph capture (under capture it returns hipErrorStreamCaptureUnsupported and
+// records nothing); later calls, captured or not, use the cached address.
+//
 // Every call on one GPU writes the same array, which keeps the last call's values.
 // Nothing in it has to start at zero: a call writes every accumulator of its [m, n]
 // range before the call ends and reads none. Calls that overlap in time on one GPU (two
@@ -40,14 +44,18 @@ hipError_t stream_device(hipStream_t stream, int* device) {
   return hipStreamGetDevice(stream, device);
 }
 
-// This device's address of `scratch`, resolved on the first call for the device.
-hipError_t scratch_on(int device, int32_t** ptr) {
+// This device's address of `scratch`, resolved on the first call for the device, which
+// must not be under graph capture on `stream`.
+hipError_t scratch_on(int device, hipStream_t stream, int32_t** ptr) {
   if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
   int32_t* cached = g_scratch[device].load(std::memory_order_acquire);
   if (cached) {
     *ptr = cached;
     return hipSuccess;
   }
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (const hipError_t e = hipStreamIsCapturing(stream, &capture); e != hipSuccess) return e;
+  if (capture != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   cached = g_scratch[device].load(std::memory_order_relaxed);
   if (!cached) {
@@ -78,7 +86,7 @@ hipError_t launch_cutlass_channel_mm_noalloc(const int8_t* a, const int8_t* w, c
   int device = 0;
   if (const hipError_t e = stream_device(stream, &device); e != hipSuccess) return e;
   int32_t* ws = nullptr;
-  if (const hipError_t e = scratch_on(device, &ws); e != hipSuccess) return e;
+  if (const hipError_t e = scratch_on(device, stream, &ws); e != hipSuccess) return e;
   return launch_channel_gemm(a, w, WeightCode::kSigned, sa, sw, out, ws, m, n, k, 0, stream);
 }
 

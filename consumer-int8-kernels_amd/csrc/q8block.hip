@@ -568,8 +568,7 @@ template <class T>
 hipError_t launch_ring(const int8_t* a, const float* sa, const int8_t* w, const uint16_t* sw,
                        uint16_t* y, int m, int n, int k, hipStream_t stream) {
   auto kernel = q8_ring_kernel<T>;
-  static std::atomic<bool> configured{false};
-  if (const hipError_t e = raise_lds_limit_once(kernel, T::kLds, configured); e != hipSuccess)
+  if (const hipError_t e = prepare_lds<q8_ring_kernel<T>>(T::kLds); e != hipSuccess)
     return e;
   // One-dimensional grid: m * n <= INT_MAX keeps the tile count far below 2^31 - 1.
   const unsigned grid = unsigned((m + T::kBM - 1) / T::kBM) * unsigned((n + T::kBN - 1) / T::kBN);

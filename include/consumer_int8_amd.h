@@ -104,7 +104,9 @@ int ci8_cutlass_channel_mm(const int8_t* a, const int8_t* w, const float* a_scal
  * nothing: no hipMalloc, no allocating library call. Requires what cutlass_channel_mm
  * requires, and m * n <= 8388608 (else CI8_ERR_TOO_LARGE). Calls that overlap in time on
  * one GPU share the array and race on it (their outputs are unaffected: nothing reads
- * the array back).
+ * the array back). The first call on each GPU looks up that GPU's address of the array
+ * and must run outside HIP graph capture (under capture it returns CI8_ERR_LAUNCH and
+ * launches nothing); later calls may be captured.
  * No counterpart in the reference: it is for callers that cannot allocate the workspace
  * tensor cutlass_channel_mm needs (code under HIP graph capture, serving loops that
  * forbid allocation). */

@@ -139,6 +139,29 @@ def test_grouped_large_m_two_waves_per_simd(ops, g, m, n, k):
         assert np.array_equal(bf16_bits(out), want), replay
 
 
+@pytest.mark.parametrize("g,m,n,k,sa_offset", [
+    (3, 1027, 132, 256, 0),  # m % 4 != 0: groups' row scales not on 16-byte boundaries
+    (2, 1024, 132, 256, 1),  # a_scale viewed 4 bytes past a 16-byte boundary
+    (3, 1028, 132, 384, 0),  # m % 4 == 0 and aligned: the two-waves-per-SIMD kernel
+])
+def test_grouped_large_m_row_scale_alignment(ops, g, m, n, k, sa_offset):
+    """The M >= 1024 kernel copies row scales four rows (16 bytes) at a time; shapes and
+    a_scale views it cannot copy that way (a copy would straddle a group boundary, be
+    misaligned or run past the end of a_scale) take the row-by-row kernel. Either way the
+    output is the oracle's, bit for bit, including the last group's last rows."""
+    rng = np.random.default_rng(g * 7919 + m + n + k + sa_offset)
+    a_np, w_np, sa_np, sw_np = grouped_inputs(rng, g, m, n, k, signed_scales=True)
+    sa_store = torch.full((g * m + sa_offset,), float("nan"), device="cuda")
+    sa = sa_store[sa_offset:].view(g, m)
+    sa.copy_(to_dev(sa_np))
+    assert sa.is_contiguous() and sa.data_ptr() % 16 == 4 * sa_offset % 16
+    out, buf = with_guard((m, n), torch.bfloat16, float("nan"))
+    ops.grouped_summed_mm(to_dev(a_np), to_dev(w_np), sa, to_dev(sw_np), out)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(out), O.grouped_summed_mm(a_np, sa_np, w_np, sw_np))
+    assert guard_intact(buf, float("nan"))
+
+
 def test_grouped_rejections(ops):
     dev = "cuda"
     a = torch.zeros(2, 8, 64, dtype=torch.int8, device=dev)

@@ -64,17 +64,75 @@ def test_noalloc_matches_cutlass_on_two_calls(ops, lib, first, second):
     run_both(lib, rng, *second, oracle_check=True)
 
 
-def test_noalloc_rejects_beyond_scratch_without_launching(ops, lib):
-    from consumer_int8 import _abi
+FIRST_CALL_UNDER_CAPTURE = r"""
+import numpy as np
+import torch
+from consumer_int8 import _abi
 
-    out = torch.full((4,), 1.0, device="cuda", dtype=torch.bfloat16)
-    big = 1 << 20
-    status = lib.ci8_cutlass_channel_mm_noalloc(big, big, big, big, out.data_ptr(), 4096,
-                                                4096, 32, None)
-    assert status == _abi.CI8_ERR_TOO_LARGE
-    assert "scratch" in _abi.last_error()
+lib = _abi.load()
+m, n, k = 64, 256, 128
+g = torch.Generator().manual_seed(3)
+a = torch.randint(-127, 128, (m, k), dtype=torch.int8, generator=g).cuda()
+w = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g).cuda()
+sa = (torch.rand(m, generator=g) / 127).cuda()
+sw = (torch.rand(n, generator=g) / 127).to(torch.bfloat16).cuda()
+out = torch.zeros(m, n, device="cuda", dtype=torch.bfloat16)
+ref = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+ws = torch.empty(m, n, device="cuda", dtype=torch.int32)
+
+
+def call(target):
+    stream = torch.cuda.current_stream().cuda_stream
+    return lib.ci8_cutlass_channel_mm_noalloc(a.data_ptr(), w.data_ptr(), sa.data_ptr(),
+                                              sw.data_ptr(), target.data_ptr(), m, n, k, stream)
+
+
+# The process's first call, under capture: refused before any HIP work is recorded.
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    out.zero_()
+    status = call(out)
+assert status == _abi.CI8_ERR_LAUNCH, status
+assert "outside graph capture" in _abi.last_error(), _abi.last_error()
+# An eager call sets up the device; a captured call then works and replays exactly.
+_abi.check(call(out))
+_abi.check(lib.ci8_cutlass_channel_mm(a.data_ptr(), w.data_ptr(), sa.data_ptr(), sw.data_ptr(),
+                                      ws.data_ptr(), ref.data_ptr(), m, n, k,
+                                      torch.cuda.current_stream().cuda_stream))
+torch.cuda.synchronize()
+assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    _abi.check(call(out))
+for replay in range(2):
+    out.fill_(7.0)
     torch.cuda.synchronize()
-    assert bool((out == 1.0).all())
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), replay
+print("first-call-under-capture: ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture_is_refused(ops, lib):
+    """In a fresh process (a child, started after this one has initialised the GPU; no
+    exec), the first call on the device is made under graph capture: it is refused with a
+    clear error and records nothing; after one eager call, captured calls replay exactly.
+    (Calls past the scratch limit are refused on the host; tests/test_abi.py checks that
+    without a GPU.)"""
+    import os
+    import subprocess
+    import sys
+
+    from tests.conftest import PKG, REPO
+
+    env = dict(os.environ)
+    env["PYTHONPATH"] = os.pathsep.join([str(REPO), str(PKG), env.get("PYTHONPATH", "")])
+    print("noalloc first call under capture (child process)", flush=True)
+    result = subprocess.run([sys.executable, "-c", FIRST_CALL_UNDER_CAPTURE], cwd=str(REPO),
+                            env=env, capture_output=True, text=True, timeout=240)
+    assert result.returncode == 0, result.stdout[-2000:] + result.stderr[-4000:]
+    assert "first-call-under-capture: ok" in result.stdout
 
 
 def test_noalloc_graph_replays(ops, lib):
