@@ -24,6 +24,15 @@ hipBLASLt, INT32 output) on the headline shape and inputs, for reference; and
 `cpu_baseline`, the reference's torch CPU math for the same step on a bounded row slice,
 on this host's cores.
 
+Inputs of the step are generated on the host from recorded seeds (`seeds`) and copied to
+the device. After the timed region the run checks its own output, as the reference
+microbenchmark does before reporting a time (benchmarks/microbench.py:205-214, :296-303):
+the leading rows of one step are recomputed by the reference's CPU math on the same host
+tensors (the cpu_baseline sample, or 64 rows without it), and the GPU's codes, row scales,
+INT32 products (cutlass_channel_mm's workspace) and BF16 outputs of those rows must equal
+them bit for bit; fused_channel_mm must equal cutlass_channel_mm over the whole output.
+The result is the `parity` record; any mismatch makes the script exit with status 1.
+
 Before the W warm-up steps the same step runs untimed for `--condition-seconds` (0.15 s),
 because the chip ramps its clock over tens of milliseconds after idle; the count is
 reported as `conditioning`. The timed region is exactly K steps. The two other
@@ -86,21 +95,46 @@ def parse_args():
     return p.parse_args()
 
 
-def make_inputs(torch, gen, copies_w=3, copies_x=3):
+SEED_X = 20261011        # activation copy i uses SEED_X + i
+SEED_W = 20261111        # weight copy i uses SEED_W + i
+SEED_SW = 20261211       # channel scales
+
+
+def host_activations(torch, seed):
+    """configs[2]'s activations on the host: BF16 [M, K] ~ N(0,1), 0.1% of the channels x50."""
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=gen, dtype=torch.float32)
+    cols = torch.randperm(K, generator=gen)[: max(1, K // 1000)]
+    x[:, cols] *= 50
+    return x.to(torch.bfloat16)
+
+
+def host_weights(torch, seed):
+    gen = torch.Generator().manual_seed(seed)
+    return torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8)
+
+
+def host_channel_scales(torch, seed):
+    gen = torch.Generator().manual_seed(seed)
+    return (torch.rand(N, generator=gen) * 9e-3 + 1e-3).to(torch.bfloat16)
+
+
+def make_inputs(torch, copies_w=3, copies_x=3):
+    """The step's inputs, generated on the host from the SEED_* seeds and copied to the
+    device; copy 0 of the host tensors is kept for the parity check and the CPU baseline."""
     dev = "cuda"
-    xs = []
-    for _ in range(copies_x):
-        x = torch.randn(M, K, generator=gen, device=dev, dtype=torch.float32)
-        cols = torch.randperm(K, generator=gen, device=dev)[: max(1, K // 1000)]
-        x[:, cols] *= 50
-        xs.append(x.to(torch.bfloat16))
-    ws = [torch.randint(-127, 128, (N, K), generator=gen, device=dev, dtype=torch.int8)
-          for _ in range(copies_w)]
-    sw = (torch.rand(N, generator=gen, device=dev) * 9e-3 + 1e-3).to(torch.bfloat16)
+    host = {"x": host_activations(torch, SEED_X), "w": host_weights(torch, SEED_W),
+            "sw": host_channel_scales(torch, SEED_SW)}
+    xs = [host["x"].to(dev)] + [host_activations(torch, SEED_X + i).to(dev)
+                                for i in range(1, copies_x)]
+    ws = [host["w"].to(dev)] + [host_weights(torch, SEED_W + i).to(dev)
+                                for i in range(1, copies_w)]
+    sw = host["sw"].to(dev)
     codes = [torch.empty(M, K, device=dev, dtype=torch.int8) for _ in range(copies_x)]
     sa = torch.empty(M, device=dev, dtype=torch.float32)
     out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
-    return xs, ws, sw, codes, sa, out
+    torch.cuda.synchronize()
+    return host, xs, ws, sw, codes, sa, out
 
 
 def condition(torch, calls, seconds=0.15):
@@ -227,44 +261,43 @@ def _cpu_model() -> str:
     return platform.processor() or platform.machine()
 
 
-def cpu_baseline(budget_s: float) -> dict:
-    """The reference's own CPU path for the step, in torch on this host's cores.
+def reference_cpu_rows(torch, x, w, sw):
+    """The reference's CPU path for rows `x` [rows, K] of the step, in torch.
 
     Quantizer: benchmarks/microbench_quantize.py:75-76 (FP32 row max / 127 floored at
-    1e-20, then round and clamp to +-127). GEMM: tests/test_cuda_ops.py:596-599 (INT32
-    matmul `a.int() @ w.int().T`, then the FP32 epilogue row scale first, channel scale
-    second, rounded to BF16). The full 4096-row step takes minutes on a CPU, so a
-    leading slice of rows is timed (sized to about `budget_s` seconds) and the rate is
-    reported per op, i.e. extrapolated by 4096 / rows to the whole step.
-    """
-    import torch
+    1e-20, then round half to even and clamp to +-127). GEMM: tests/test_cuda_ops.py:596-599
+    (INT32 matmul `a.int() @ w.int().T`, then the FP32 epilogue: row scale first, channel
+    scale second, rounded to BF16). Returns codes, scales, INT32 products and outputs."""
+    scale = (x.float().abs().amax(-1) / 127).clamp_min(1e-20)
+    codes = (x.float() / scale[:, None]).round().clamp(-127, 127).to(torch.int8)
+    integer = codes.int() @ w.int().T
+    out = (integer.float() * scale[:, None] * sw.float()[None, :]).to(torch.bfloat16)
+    return {"codes": codes, "scale": scale, "integer": integer, "out": out}
 
+
+def cpu_baseline(torch, host, budget_s: float) -> tuple[dict, dict]:
+    """The reference's own CPU path for the step (reference_cpu_rows) on this host's cores,
+    on the same host tensors the GPU step uses. The full 4096-row step takes minutes on a
+    CPU, so a leading slice of rows is timed (sized to about `budget_s` seconds) and the rate
+    is reported per op, i.e. extrapolated by 4096 / rows to the whole step. Returns the
+    baseline record and the slice's results (for the parity check)."""
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    gen = torch.Generator().manual_seed(20261011)
-    w = torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8)
-    sw = (torch.rand(N, generator=gen) * 9e-3 + 1e-3).to(torch.bfloat16)
-    cols = torch.randperm(K, generator=gen)[: max(1, K // 1000)]
+    x, w, sw = host["x"], host["w"], host["sw"]
 
     def run(rows):
-        x = torch.randn(rows, K, generator=gen)
-        x[:, cols] *= 50
-        x = x.to(torch.bfloat16)
         t0 = time.perf_counter()
-        scale = (x.float().abs().amax(-1) / 127).clamp_min(1e-20)
-        codes = (x.float() / scale[:, None]).round().clamp(-127, 127).to(torch.int8)
-        integer = codes.int() @ w.int().T
-        out = (integer.float() * scale[:, None] * sw.float()[None, :]).to(torch.bfloat16)
+        ref = reference_cpu_rows(torch, x[:rows], w, sw)
         elapsed = time.perf_counter() - t0
-        assert out.shape == (rows, N)
-        return elapsed
+        assert ref["out"].shape == (rows, N)
+        return elapsed, ref
 
     rows = 32
-    elapsed = run(rows)
+    elapsed, _ = run(rows)
     rows = int(min(M, max(32, rows * budget_s / max(elapsed, 1e-3))))
-    elapsed = run(rows)
+    elapsed, ref = run(rows)
     tops = 2 * rows * N * K / elapsed / 1e12
-    return {
+    record = {
         "value": round(tops, 5),
         "unit": "TOPS",
         "cores": cores,
@@ -272,12 +305,53 @@ def cpu_baseline(budget_s: float) -> dict:
         "path": "the reference's torch CPU math, restated here",
         "sample": f"reference torch CPU math (benchmarks/microbench_quantize.py:75-76 quantizer, "
                   f"tests/test_cuda_ops.py:596-599 INT32 matmul + FP32 epilogue) on the first "
-                  f"{rows} of {M} rows (K={K}, N={N}) in {elapsed:.2f} s, extrapolated "
-                  f"x{M / rows:.2f} to the full step ({M / rows * elapsed:.1f} s)",
+                  f"{rows} of {M} rows (K={K}, N={N}) of the GPU step's own inputs, in "
+                  f"{elapsed:.2f} s, extrapolated x{M / rows:.2f} to the full step "
+                  f"({M / rows * elapsed:.1f} s)",
         "cpu_model": _cpu_model(),
         "torch": torch.__version__,
         "threads": torch.get_num_threads(),
     }
+    return record, ref
+
+
+def parity_record(torch, gpu: dict, ref: dict, fused_equals_cutlass: bool) -> dict:
+    """Bit-for-bit comparison of the GPU's leading rows (host copies of codes, row scales,
+    INT32 products and BF16 outputs) with the reference's CPU results for the same rows."""
+    rows = ref["out"].shape[0]
+    checks = {
+        "codes": torch.equal(gpu["codes"][:rows], ref["codes"]),
+        "row_scales": torch.equal(gpu["scale"][:rows].view(torch.int32),
+                                  ref["scale"].view(torch.int32)),
+        "int32_products": torch.equal(gpu["integer"][:rows], ref["integer"]),
+        "bf16_outputs": torch.equal(gpu["out"][:rows].view(torch.int16),
+                                    ref["out"].view(torch.int16)),
+        "fused_equals_cutlass": bool(fused_equals_cutlass),
+    }
+    return {"rows_compared": rows, "of_rows": M, "input_copy": 0,
+            "against": "the reference's torch CPU math on the same host tensors",
+            **checks, "all_equal": all(checks.values())}
+
+
+def parity_check(torch, ops, xs, ws, sw, ref) -> dict:
+    """One more step on copy 0 of the inputs (untimed): its leading rows against the
+    reference's CPU results for the same host tensors (`ref`), bit for bit, and
+    fused_channel_mm against cutlass_channel_mm on the same codes over the whole output."""
+    rows = ref["out"].shape[0]
+    codes = torch.empty(M, K, device="cuda", dtype=torch.int8)
+    sa = torch.empty(M, device="cuda", dtype=torch.float32)
+    fused = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    cut = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    workspace = torch.empty(M, N, device="cuda", dtype=torch.int32)
+    ops.quantize_rows(xs[0], codes, sa)
+    ops.fused_channel_mm(codes, ws[0], sa, sw, fused, 0)
+    ops.cutlass_channel_mm(codes, ws[0], sa, sw, workspace, cut)
+    torch.cuda.synchronize()
+    same = torch.equal(fused.view(torch.int16), cut.view(torch.int16))
+    gpu = {"codes": codes[:rows].cpu(), "scale": sa[:rows].cpu(),
+           "integer": workspace[:rows].cpu(), "out": fused[:rows].cpu()}
+    del codes, sa, fused, cut, workspace
+    return parity_record(torch, gpu, ref, same)
 
 
 def main() -> int:
@@ -296,8 +370,8 @@ def main() -> int:
     props = torch.cuda.get_device_properties(0)
     cus = props.multi_processor_count
     peak_tops = PEAK_INT8_TOPS * cus / 256
-    gen = torch.Generator(device="cuda").manual_seed(20261011)
-    xs, ws, sw, codes, sa, out = make_inputs(torch, gen)
+    host, xs, ws, sw, codes, sa, out = make_inputs(torch)
+    gen = torch.Generator(device="cuda").manual_seed(20261011)  # the extras' own inputs
 
     def step(i):
         x, c, w = xs[i % len(xs)], codes[i % len(codes)], ws[i % len(ws)]
@@ -352,8 +426,11 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded on device): x BF16 N(0,1) with 0.1% channels x50, "
-                "w INT8 U[-127,127], w_scale BF16 U[1e-3,1e-2]",
+        "data": "synthetic (seeded on the host, copied to the device): x BF16 N(0,1) with "
+                "0.1% channels x50, w INT8 U[-127,127], w_scale BF16 U[1e-3,1e-2]",
+        "seeds": {"x": [SEED_X + i for i in range(len(xs))],
+                  "w": [SEED_W + i for i in range(len(ws))], "w_scale": SEED_SW,
+                  "generator": "torch.Generator() (CPU): randn / randperm / randint / rand"},
         "config": {"workload": "configs[2] prefill projection: quantize_rows BF16[4096,5120] "
                                "+ fused_channel_mm M=4096 K=5120 N=17408",
                    "M": M, "K": K, "N": N, "schedule": 0},
@@ -478,11 +555,11 @@ def main() -> int:
         del a4, s4, w4, o4
         # configs[3]'s activation producer: SwiGLU of BF16 [16384, 2*17408] quantized per
         # row (silu_mul_quantize), and the unquantized silu_mul, both far beyond the MALL.
-        xs = torch.randn(M4, 2 * K4, generator=gen, device="cuda").to(torch.bfloat16)
+        x_glu = torch.randn(M4, 2 * K4, generator=gen, device="cuda").to(torch.bfloat16)
         cs = torch.empty(M4, K4, device="cuda", dtype=torch.int8)
         ss = torch.empty(M4, device="cuda")
-        ops.silu_mul_quantize(xs, cs, ss)
-        mean_us, _ = time_kernel(torch, [lambda: ops.silu_mul_quantize(xs, cs, ss)], 3, batch=4)
+        ops.silu_mul_quantize(x_glu, cs, ss)
+        mean_us, _ = time_kernel(torch, [lambda: ops.silu_mul_quantize(x_glu, cs, ss)], 3, batch=4)
         bs = 4 * M4 * K4 + M4 * K4 + 4 * M4
         extras["silu_mul_quantize_cfg4"] = {"bound": "hbm", "achieved": round(bs / (mean_us * 1e-6) / 1e9, 1),
                                             "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -490,14 +567,14 @@ def main() -> int:
                                             "mean_us": round(mean_us, 2), "bytes": bs}
         del cs, ss
         act = torch.empty(M4, K4, device="cuda", dtype=torch.bfloat16)
-        ops.silu_mul(xs, act)
-        mean_us, _ = time_kernel(torch, [lambda: ops.silu_mul(xs, act)], 3, batch=4)
+        ops.silu_mul(x_glu, act)
+        mean_us, _ = time_kernel(torch, [lambda: ops.silu_mul(x_glu, act)], 3, batch=4)
         bs = 4 * M4 * K4 + 2 * M4 * K4
         extras["silu_mul_cfg4"] = {"bound": "hbm", "achieved": round(bs / (mean_us * 1e-6) / 1e9, 1),
                                    "peak": PEAK_HBM_GBS, "unit": "GB/s",
                                    "frac": round(bs / (mean_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
                                    "mean_us": round(mean_us, 2), "bytes": bs}
-        del xs, act
+        del x_glu, act
         # unpack_allspark of configs[3]'s weights [5120, 17408]: 3 packed copies rotate
         # (267 MB of input plus the 89 MB output exceed the MALL).
         pk = [torch.randint(0, 256, (N4, K4), generator=gen, device="cuda", dtype=torch.uint8)
@@ -642,11 +719,17 @@ def main() -> int:
         del src, dst
 
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        result["cpu_baseline"], ref = cpu_baseline(torch, host, args.cpu_seconds)
     else:
         result["cpu_baseline"] = None
+        ref = reference_cpu_rows(torch, host["x"][:64], host["w"], host["sw"])
+    result["parity"] = parity_check(torch, ops, xs, ws, sw, ref)
 
     print(json.dumps(result), flush=True)
+    if not result["parity"]["all_equal"]:
+        print("bench.py: the GPU output differs from the reference's CPU results "
+              f"({result['parity']})", file=sys.stderr)
+        return 1
     return 0
 
 
