@@ -100,6 +100,10 @@ __device__ __forceinline__ u32x4 load16(const void* p) {
     return *reinterpret_cast<const u32x4*>(p);
 }
 
+// Cache-policy operand of a buffer load that marks it nontemporal (the nt bit of gfx950's
+// cache-policy field): for streams read once, such as a GEMV's weights.
+constexpr int kBufferLoadNontemporal = 2;
+
 // Raw buffer resource over `bytes` bytes starting at `base`. Loads at byte offsets
 // >= bytes return zero, which covers row and column tails without branches.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {

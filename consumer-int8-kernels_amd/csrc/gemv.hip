@@ -497,7 +497,13 @@ __global__ void __launch_bounds__(C::kThreads, C::kWavesPerEU) channel_gemv_pers
 // (codes and scale), and vmcnt(kC + 1) means row r has landed. A lane dequantizes its
 // 16 codes exactly as the MFMA kernels do (bf16_rn(code * scale), packed in pairs) and
 // feeds them with x to v_dot2_f32_bf16; the 64 lane sums meet by a butterfly, in FP32.
-// Rows past N load nothing (range-checked offsets) and store nothing.
+// Rows past N load nothing (range-checked offsets) and store nothing. The weight loads are
+// nontemporal: every byte is read once (measured on MI355X at K = 5120, N = 17408: 17.0
+// against 17.9 us with plain loads, identical outputs; the balanced-span kernel below
+// keeps plain loads, since neighbouring waves read the two halves of a 128-byte line
+// there and nontemporal loads made it 18% slower). This kernel also runs M = 2..4
+// correctly (one dequantization, M dot products) but loses to the span kernel there:
+// 19.1 / 22.2 / 24.0 against 18.7 - 18.9 us at K = 5120, N = 17408.
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
@@ -535,7 +541,7 @@ __global__ void __launch_bounds__(256) channel_gemv_rows_kernel(
       wr[slot][c] = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                      w_rsrc, row < n && col < k ? uint32_t(row) * uint32_t(k) + uint32_t(col)
-                                                : kOutOfRange, 0, 0));
+                                                : kOutOfRange, 0, kBufferLoadNontemporal));
     }
     sr[slot] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, row < n ? uint32_t(row) * 2u
                                                                    : kOutOfRange, 0, 0);
