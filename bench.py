@@ -41,6 +41,7 @@ untimed launches of their own before they are timed.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-extras]
                       [--copy-calibration] [--condition-seconds S]
+       python bench.py --phase-profile   (the GEMM's per-phase cycle table; no bench line)
 """
 
 from __future__ import annotations
@@ -89,6 +90,9 @@ def parse_args():
                         "steady clock (the first ~100 steps after idle run up to 18%% slower)")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="approximate CPU time budget of the cpu_baseline sample")
+    p.add_argument("--phase-profile", action="store_true",
+                   help="print the persistent GEMM's per-phase cycle table at configs[2] "
+                        "(clock-stamped build of the same kernel) instead of the bench line")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a plain 512 MiB device copy three times (a kernel of known "
                         "traffic that scales FETCH_SIZE / WRITE_SIZE counters)")
@@ -359,6 +363,118 @@ def parity_check(torch, ops, xs, ws, sw, ref) -> dict:
     return parity_record(torch, gpu, ref, same)
 
 
+# The persistent GEMM's MFMA floor per K stage: each SIMD runs two waves, each issuing
+# TM x TN x 2 = 4 x 7 x 2 = 56 v_mfma_i32_16x16x64_i8 per stage, and one such MFMA
+# (32,768 ops) occupies a SIMD's matrix core for 16 cycles (8,192 ops/clk per CU over 4
+# SIMDs): 2 x 56 x 16 = 1,792 cycles.
+PP_BM, PP_BN, PP_BK = 256, 224, 128
+PP_STAGE_FLOOR_CYCLES = 2 * 4 * 7 * 2 * 16
+PHASES = ["memory phase (fragment reads + copies issued)", "wait for W(t+1) (group 1)",
+          "barrier 1", "compute phase (56 MFMAs)", "wait for A(t+1) (group 0)", "barrier 2"]
+TILE_PHASES = ["tile start (scale loads, zeroing, group 1's offset barrier)",
+               "tile end (drain barriers, next tile's first copies, epilogue)"]
+
+
+def phase_profile(torch, ops, xs, ws, sw, codes, sa, out, reps: int = 6) -> tuple[str, bool]:
+    """Per-phase cycle table of the persistent GEMM at configs[2] (csrc/probe_pp.hip: the
+    library's kernel source with clock stamps). Mode 1 stamps only each workgroup's start
+    and end (shader clock and the 100 MHz wall clock); mode 2 also sums each wave's cycles
+    per phase kind for wave 0 (copies A) and wave 4 (copies W). Launches rotate over the
+    bench's input copies; both modes' last output must equal fused_channel_mm's bit for bit."""
+    import ctypes
+
+    lib = ctypes.CDLL(str(REPO / "consumer-int8-kernels_amd" / "consumer_int8" / "libci8_probe.so"))
+    lib.ci8probe_pp_gemm_stamped.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 4 + [
+        ctypes.c_void_p, ctypes.c_void_p]
+    shader_khz, wall_khz = ctypes.c_int(0), ctypes.c_int(0)
+    assert lib.ci8probe_clock_rates(ctypes.byref(shader_khz), ctypes.byref(wall_khz)) == 0
+    grid = lib.ci8probe_pp_grid(M, N)
+    tiles = -(-M // PP_BM) * -(-N // PP_BN)
+    ns = -(-K // PP_BK)
+    my_tiles = torch.tensor([(tiles - b + grid - 1) // grid for b in range(grid)], dtype=torch.float64)
+    ops.quantize_rows(xs[0], codes[0], sa)
+    want = torch.empty_like(out)
+    ops.fused_channel_mm(codes[0], ws[0], sa, sw, want, 0)
+    record = torch.zeros(reps, grid * 24, dtype=torch.int64, device="cuda")
+
+    def stamped(i, mode, rec):
+        j = i % len(ws)
+        assert lib.ci8probe_pp_gemm_stamped(
+            codes[j % len(codes)].data_ptr(), ws[j].data_ptr(), sa.data_ptr(), sw.data_ptr(),
+            out.data_ptr(), M, N, K, mode, rec.data_ptr(),
+            torch.cuda.current_stream().cuda_stream) == 0
+
+    def product(i):
+        j = i % len(ws)
+        ops.fused_channel_mm(codes[j % len(codes)], ws[j], sa, sw, out, 0)
+
+    def timed(launch):
+        condition(torch, [lambda i=i: launch(i, 0) for i in range(len(ws))], 0.15)
+        events = []
+        for r in range(reps):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            launch(r, r)
+            end.record()
+            events.append((start, end))
+        torch.cuda.synchronize()
+        return statistics.mean(s.elapsed_time(e) * 1e3 for s, e in events)
+
+    kernel_us = {0: timed(lambda i, r: product(i))}
+    recs, exact = {}, True
+    for mode in (1, 2):
+        kernel_us[mode] = timed(lambda i, r, mode=mode: stamped(i, mode, record[r]))
+        recs[mode] = record.view(reps, grid, 24).cpu().double()
+        out.zero_()
+        stamped(0, mode, record[0])
+        torch.cuda.synchronize()
+        exact = exact and torch.equal(out.view(torch.int16), want.view(torch.int16))
+
+    r1 = recs[1]
+    cycles = r1[:, :, 1] - r1[:, :, 0]
+    mhz = cycles / (r1[:, :, 3] - r1[:, :, 2]) * wall_khz.value / 1e3
+    clock = float(mhz.median())
+    per_tile = float((cycles / my_tiles).mean())
+    floor_tile = ns * PP_STAGE_FLOOR_CYCLES
+    r2 = recs[2]
+    per_stage = [(r2[:, :, 4 + 8 * g:10 + 8 * g] / (my_tiles * ns)[:, None]).mean(dim=(0, 1))
+                 for g in (0, 1)]
+    per_tile2 = [(r2[:, :, 10 + 8 * g:12 + 8 * g] / my_tiles[:, None]).mean(dim=(0, 1))
+                 for g in (0, 1)]
+    lines = [
+        f"configs[2] M={M} K={K} N={N}: {tiles} tiles of {PP_BM}x{PP_BN} on {grid} workgroups "
+        f"({tiles / grid:.3f} rounds), {ns} K stages of {PP_BK} per tile.",
+        "",
+        "| launch | mean us | note |",
+        "|---|---|---|",
+        f"| library kernel (fused_channel_mm) | {kernel_us[0]:.1f} | no stamps |",
+        f"| mode 1 (start/end stamps) | {kernel_us[1]:.1f} | same code plus 4 clock reads per workgroup |",
+        f"| mode 2 (per-phase stamps) | {kernel_us[2]:.1f} | 8 clock reads per stage per wave: slower than the kernel it describes |",
+        "",
+        f"Mode 1: shader clock {clock:.0f} MHz (median over workgroups, cycles / wall-clock "
+        f"ticks); {per_tile:,.0f} cycles per tile against the MFMA floor of "
+        f"{floor_tile:,} ({ns} x {PP_STAGE_FLOOR_CYCLES}): {floor_tile / per_tile:.3f} of "
+        f"the matrix cores' time at that clock.",
+        "",
+        "Mode 2, cycles per K stage (mean over workgroups and stages; floor "
+        f"{PP_STAGE_FLOOR_CYCLES}):",
+        "",
+        "| phase | wave 0 (group 0, copies A) | wave 4 (group 1, copies W) |",
+        "|---|---|---|",
+    ]
+    for i, name in enumerate(PHASES):
+        lines.append(f"| {name} | {per_stage[0][i]:.0f} | {per_stage[1][i]:.0f} |")
+    lines.append(f"| **K stage total** | **{per_stage[0].sum():.0f}** | **{per_stage[1].sum():.0f}** |")
+    lines += ["", "Mode 2, cycles per tile outside the K loop:", "",
+              "| phase | wave 0 | wave 4 |", "|---|---|---|"]
+    for i, name in enumerate(TILE_PHASES):
+        lines.append(f"| {name} | {per_tile2[0][i]:.0f} | {per_tile2[1][i]:.0f} |")
+    total2 = [float(per_stage[g].sum() * ns + per_tile2[g].sum()) for g in (0, 1)]
+    lines.append(f"| **tile total (K loop + outside)** | **{total2[0]:,.0f}** | **{total2[1]:,.0f}** |")
+    lines += ["", f"Outputs of both stamped modes equal fused_channel_mm's bit for bit: {exact}."]
+    return "\n".join(lines), exact
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -376,6 +492,10 @@ def main() -> int:
     cus = props.multi_processor_count
     peak_tops = PEAK_INT8_TOPS * cus / 256
     host, xs, ws, sw, codes, sa, out = make_inputs(torch)
+    if args.phase_profile:
+        table, exact = phase_profile(torch, ops, xs, ws, sw, codes, sa, out)
+        print(table)
+        return 0 if exact else 1
     gen = torch.Generator(device="cuda").manual_seed(20261011)  # the extras' own inputs
 
     def step(i):

@@ -88,12 +88,16 @@ def build_library(jobs: int = 8) -> Path:
 
 
 def build_probe() -> Path:
-    obj = BUILD_DIR / "probe.o"
+    """bench.py's measurement library: the MFMA/HBM probes (probe.hip) and the persistent
+    GEMM with clock stamps (probe_pp.hip, built with gemm_pp.hip's flags). It links the
+    drop-in library for device_cu_count."""
     BUILD_DIR.mkdir(exist_ok=True)
-    _compile(CSRC / "probe.hip", obj)
+    objects = [_compile(CSRC / name, BUILD_DIR / (Path(name).stem + ".o"))
+               for name in ("probe.hip", "probe_pp.hip")]
     target = OUT_DIR / "libci8_probe.so"
     tmp = target.with_suffix(".so.tmp")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), str(obj),
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects),
+          f"-L{OUT_DIR}", "-lci8_amd", "-Wl,-rpath,$ORIGIN",
           f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}",
           "-Wl,-soname,libci8_probe.so"])
     os.replace(tmp, target)

@@ -1,0 +1,378 @@
+// The persistent two-waves-per-SIMD INT8 GEMM kernel (the design is described in
+// gemm_pp.hip). It lives in this header so that a measurement build of the same source
+// (probe_pp.hip, with per-phase clock stamps) compiles exactly the library's code path.
+#pragma once
+#include <type_traits>
+
+#include "ci8_device.h"
+#include "launch.h"
+
+namespace ci8 {
+namespace {
+
+constexpr int kXcds = 8;
+
+struct PPConfig {
+  static constexpr int BM = 256, BN = 224, BK = 128;
+  static constexpr int kWaves = 8, kThreads = 512;
+  static constexpr int WM = 4;                        // waves along m (per group)
+  static constexpr int TM = BM / WM / 16;             // 4 m blocks per wave
+  static constexpr int TN = BN / 2 / 16;              // 7 n blocks per wave
+  static constexpr int kABlocks = BM * BK / 1024;     // 32 copies of A per stage
+  static constexpr int kWBlocks = BN * BK / 1024;     // 28 copies of W per stage
+  static constexpr int kCopies = kABlocks / WM;       // per wave per stage (8)
+  static constexpr int kAStage = BM * BK;             // 32 KB
+  static constexpr int kWStage = BN * BK;             // 28 KB
+  static constexpr int kWBase = 2 * kAStage;          // A ring: 2 slots, W ring: 3 slots
+  static constexpr int kJunk = kWBase + 3 * kWStage;  // 148 KB
+  static constexpr int kRingBytes = kJunk + 1024;
+  // Epilogue staging (reuses the ring): each wave's 64 x 112 BF16 outputs at a row
+  // stride of 240 bytes (60 dwords: 16 rows written by one ds_write_b64 start in
+  // distinct banks).
+  static constexpr int kEpiRowBytes = (BN / 2) * 2 + 16;
+  static constexpr int kEpiPassBytes = 16 * kEpiRowBytes;  // one 16-row block per wave
+  static constexpr int kLdsBytes = kRingBytes;
+  // m tiles per raster group: each XCD's 32 tiles of a round then cover 4 m x 8 n
+  // tiles (measured on MI355X against 2, 8 and 16: configs[2] 277-278 against 280-286
+  // us at 8; configs[3] 1,108-1,110 against 1,152-1,154 us).
+  static constexpr int GROUP_M = 4;
+  static_assert(kCopies * WM == kABlocks && (kCopies - 1) * WM == kWBlocks, "copies");
+  static_assert(3 * (kCopies - 1) < 2 * (TM + TN), "copies fit between the fragment reads");
+  static_assert(kLdsBytes <= 160 * 1024, "LDS");
+  static_assert(kWaves * kEpiPassBytes <= kAStage, "epilogue passes fit in A slot 1");
+};
+
+__device__ __forceinline__ i32x4 lds16(const char __attribute__((address_space(3)))* p) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) i32x4*>(p);
+}
+__device__ __forceinline__ void barrier_fenced() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// kStamps (a measurement build only; the library uses 0): 1 records each workgroup's
+// shader-clock and wall-clock times at start and end, 2 also sums, per wave, the cycles of
+// each phase kind (PhaseStamp) and records those of waves 0 and 4 (one of each group).
+// Layout of `stamps`, 24 values per workgroup: wave 0's clock start, clock end, wall
+// start and wall end, the 8 sums of wave 0, the 8 of wave 4, then wave 4's clock start
+// and end and two zeros. Each wave's sums add up to its own clock end minus its clock
+// start. Reading s_memtime waits for the read, so mode 2 runs slower than the kernel it
+// describes.
+enum PhaseStamp {
+  kStampMemory, kStampWaitW, kStampBarrier1, kStampCompute, kStampWaitA, kStampBarrier2,
+  kStampTileStart, kStampTileEnd, kStampKinds
+};
+
+template <bool kExactK, WeightCode kCode, int kStamps = 0>
+__global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
+    const int8_t* __restrict__ a, const int8_t* __restrict__ w, const float* __restrict__ sa,
+    const uint16_t* __restrict__ sw, uint16_t* __restrict__ out, int m, int n, int k,
+    bool out16, int64_t* __restrict__ stamps) {
+  using C = PPConfig;
+  extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
+  auto* lds = (char __attribute__((address_space(3)))*)(lds_raw);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave % C::WM, group = wave / C::WM;
+  const bool copies_a = group == 0;
+
+  // Work item -> tile: items are dealt to the 8 XCDs round-robin (workgroup b runs on
+  // XCD b % 8 and takes items b, b + grid, ...; the grid is a multiple of 8 when it
+  // fills the chip), so map the items of each XCD to a contiguous range of a grouped
+  // raster of GROUP_M m tiles: tiles that run together on one XCD share panels in its L2.
+  const int tiles_n = (n + C::BN - 1) / C::BN;
+  const int tiles_m = (m + C::BM - 1) / C::BM;
+  const int tiles = tiles_n * tiles_m;
+  const int grid = int(gridDim.x);
+  const int my_tiles = (tiles - int(blockIdx.x) + grid - 1) / grid;
+  auto tile_of = [&] __device__(int item, int& m0, int& n0) __attribute__((always_inline)) {
+    const int per = tiles / kXcds, extra = tiles % kXcds;
+    const int xcd = item % kXcds, idx = item / kXcds;
+    const int logical =
+        (xcd < extra ? xcd * (per + 1) : extra * (per + 1) + (xcd - extra) * per) + idx;
+    const int group_span = C::GROUP_M * tiles_n;
+    const int first_m = (logical / group_span) * C::GROUP_M;
+    const int group_rows = min(tiles_m - first_m, C::GROUP_M);
+    m0 = (first_m + (logical % group_span) % group_rows) * C::BM;
+    n0 = ((logical % group_span) / group_rows) * C::BN;
+  };
+
+  const auto a_rsrc = make_rsrc(a, uint32_t(m) * uint32_t(k));
+  const auto w_rsrc = make_rsrc(w, uint32_t(n) * uint32_t(k));
+  const auto c_rsrc = copies_a ? a_rsrc : w_rsrc;
+  const int ns = (k + C::BK - 1) / C::BK;
+
+  // Copy i of a wave brings block b = 4i + wave % 4 of its operand's stage (8 rows x 128
+  // bytes): lane -> row 8b + lane / 8, LDS chunk slot lane % 8 holding logical chunk
+  // slot ^ (row % 8). The stage's K offset goes in soffset; the per-lane row offsets
+  // depend on the tile and are set when a tile's first copies are issued.
+  const int sub = wave % C::WM;
+  const int c_row = lane >> 3;
+  const int c_chunk = (lane & 7) ^ c_row;
+  uint32_t c_off[C::kCopies];
+  auto set_copy_tile = [&] __device__(int m0, int n0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < C::kCopies; ++i) {
+      const int row = (copies_a ? m0 : n0) + (i * C::WM + sub) * 8 + c_row;
+      const bool valid = (copies_a || i < C::kCopies - 1) && row < (copies_a ? m : n);
+      c_off[i] = valid ? uint32_t(row) * uint32_t(k) + uint32_t(c_chunk * 16) : kOutOfRange;
+    }
+  };
+  // LDS destination of copy i into ring slot `slot`: c_dst0 + slot * c_stride + 4096 i
+  // (integer arithmetic on wave-uniform values), except a W wave's eighth (junk KiB).
+  const int c_dst0 = (copies_a ? 0 : C::kWBase) + sub * 1024;
+  const int c_stride = copies_a ? C::kAStage : C::kWStage;
+  auto copy = [&] __device__(int dst, int t, int i) __attribute__((always_inline)) {
+    int to = dst + i * C::WM * 1024;
+    if (i == C::kCopies - 1) to = copies_a ? to : C::kJunk;
+    const int k0 = t * C::BK;
+    uint32_t off = c_off[i];
+    if (!kExactK && off != kOutOfRange && k0 + c_chunk * 16 >= k) off = kOutOfRange;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c_rsrc, reinterpret_cast<lds_void*>(lds + to), 16,
+                                             off, k0, 0, 0);
+  };
+  // A tile's first copies: A(0) (group 0) into A slot 0, W(0) and W(1) (group 1) into
+  // W slots 0 and 1.
+  auto first_copies = [&] __device__() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < C::kCopies; ++i) copy(c_dst0, 0, i);
+    if (!copies_a && 1 < ns) {
+#pragma unroll
+      for (int i = 0; i < C::kCopies; ++i) copy(c_dst0 + c_stride, 1, i);
+    }
+  };
+
+  // Fragments: row (lane % 16) of each 16-row block at logical chunk 4h + lane / 16.
+  const int f_row = lane & 15, f_group = lane >> 4;
+  int a_base[2], w_base[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int swz = (((4 * h + f_group) ^ (f_row & 7)) * 16);
+    a_base[h] = (wm * 64 + f_row) * C::BK + swz;
+    w_base[h] = C::kWBase + (group * 112 + f_row) * C::BK + swz;
+  }
+  i32x4 af[2][C::TM], wf[2][C::TN];
+  // Memory phase: the 22 fragments of the stage in A slot a_slot and W slot w_slot, with
+  // (kCopy) this wave's 8 copies of stage copy_t into `dst` after fragment reads 0, 3,
+  // ..., 21. Stages past the end are not copied at all.
+  auto memory = [&] __device__(int a_slot, int w_slot, int dst, int copy_t, auto with_copies)
+                    __attribute__((always_inline)) {
+    constexpr bool kCopy = decltype(with_copies)::value;
+    const auto* as = lds + a_slot * C::kAStage;
+    const auto* ws = lds + w_slot * C::kWStage;
+#pragma unroll
+    for (int q = 0; q < 2 * (C::TM + C::TN); ++q) {
+      const int h = q / (C::TM + C::TN), r = q % (C::TM + C::TN);
+      if (r < C::TM)
+        af[h][r] = lds16(as + a_base[h] + r * 16 * C::BK);
+      else
+        wf[h][r - C::TM] = lds16(ws + w_base[h] + (r - C::TM) * 16 * C::BK);
+      if constexpr (kCopy)
+        if (q % 3 == 0) copy(dst, copy_t, q / 3);
+    }
+    __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+    if constexpr (kCode == WeightCode::kBiasedU8) {
+      // Biased UINT8 codes (code + 128) -> signed INT8 codes: flip each byte's top bit.
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < C::TN; ++i) wf[h][i] ^= int(0x80808080u);
+    }
+  };
+
+  i32x4 acc[C::TM][C::TN];
+  auto compute = [&] __device__() __attribute__((always_inline)) {
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < C::TN; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TM; ++j)
+          acc[j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[h][i], af[h][j], acc[j][i], 0, 0, 0);
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  if (my_tiles <= 0) return;  // uniform over the workgroup
+  int64_t phase[kStampKinds] = {};
+  int64_t last = 0, clock0 = 0, wall0 = 0;
+  if constexpr (kStamps > 0) {
+    wall0 = __builtin_amdgcn_s_memrealtime();
+    clock0 = last = __builtin_amdgcn_s_memtime();
+  }
+  // Adds the cycles since the previous stamp to phase kind `kind` (mode 2 only).
+  auto stamp = [&] __device__(int kind) __attribute__((always_inline)) {
+    if constexpr (kStamps > 1) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int64_t now = __builtin_amdgcn_s_memtime();
+      phase[kind] += now - last;
+      last = now;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  int m0, n0;
+  tile_of(int(blockIdx.x), m0, n0);
+  set_copy_tile(m0, n0);
+  first_copies();
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  barrier_fenced();
+
+  for (int r = 0; r < my_tiles; ++r) {
+    // This tile's row and channel scales, loaded now (older than any copy of the tile,
+    // so the waits of the K loop cover them).
+    float rs[C::TM];
+    u32x2 s2[C::TN];
+    {
+      const int row0 = m0 + wm * 64, col0 = n0 + group * 112;
+#pragma unroll
+      for (int j = 0; j < C::TM; ++j) {
+        const int row = row0 + j * 16 + f_row;
+        rs[j] = row < m ? sa[row] : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < C::TN; ++i) {
+        const int col = col0 + i * 16 + f_group * 4;
+        s2[i] = col < n ? *reinterpret_cast<const u32x2*>(sw + col) : u32x2{0, 0};
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < C::TM; ++j)
+#pragma unroll
+      for (int i = 0; i < C::TN; ++i) acc[j][i] = i32x4{0, 0, 0, 0};
+
+    // Stage t: group 0 copies A(t + 1) (into A slot (t + 1) % 2), group 1 W(t + 2) (into
+    // W slot (t + 2) % 3). The last stages, with nothing left to copy, issue no copies,
+    // and group 1 then waits for all of its copies instead of all but the newest stage's.
+    int w_slot = 0;   // t % 3
+    int cw_slot = 2;  // (t + 2) % 3
+    const int lead = copies_a ? 1 : 2;
+    if (group == 1) barrier_fenced();  // phase 0 is group 0's first memory phase
+    stamp(kStampTileStart);
+    for (int t = 0; t < ns; ++t) {
+      const int copy_t = t + lead;
+      const int dst = c_dst0 + (copies_a ? (t + 1) & 1 : cw_slot) * c_stride;
+      if (copy_t < ns) {  // uniform over the wave
+        memory(t & 1, w_slot, dst, copy_t, std::true_type{});
+        stamp(kStampMemory);
+        // Group 1: W(t + 1) landed (W(t + 2), just issued, may be in flight).
+        if (group == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(C::kCopies));
+      } else {
+        memory(t & 1, w_slot, dst, copy_t, std::false_type{});
+        stamp(kStampMemory);
+        if (group == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      }
+      stamp(kStampWaitW);
+      barrier_fenced();
+      stamp(kStampBarrier1);
+      compute();
+      stamp(kStampCompute);
+      // Group 0: A(t + 1), issued in the memory phase, landed.
+      if (group == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      stamp(kStampWaitA);
+      barrier_fenced();
+      stamp(kStampBarrier2);
+      w_slot = w_slot == 2 ? 0 : w_slot + 1;
+      cw_slot = cw_slot == 2 ? 0 : cw_slot + 1;
+    }
+    if (group == 0) barrier_fenced();  // phase 2 ns: group 1's last compute phase
+    barrier_fenced();                  // every wave is past its last fragment reads
+
+    // The next tile's first copies go out now, into A slot 0 and W slots 0 and 1, and
+    // land while this tile's results are stored through A slot 1. Every load of this
+    // tile has landed by now (each wave waited for its last copies); the explicit wait
+    // says so to the compiler, which otherwise waits for those first copies before the
+    // epilogue's first use of the scales loaded at the tile start.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    const int tile_m0 = m0, tile_n0 = n0;
+    const bool more = r + 1 < my_tiles;
+    if (more) {
+      tile_of(int(blockIdx.x) + (r + 1) * grid, m0, n0);
+      set_copy_tile(m0, n0);
+      first_copies();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+
+    // Epilogue through LDS, 16 rows of the wave's 64 at a time: the 16 x 112 BF16
+    // results of row block j go to the wave's 3840-byte region of A slot 1 in the MFMA
+    // layout and come back as 16-byte row chunks, so each store instruction writes whole
+    // 224-byte row pieces (14 lanes per row).
+    const int row0 = tile_m0 + wm * 64;
+    const int col0 = tile_n0 + group * 112;
+    auto* region = lds + C::kAStage + wave * C::kEpiPassBytes;
+    constexpr int kChunks = 112 / 8;  // 16-byte chunks per output row piece
+    const bool full = out16 && row0 + 64 <= m && col0 + 112 <= n && (n % 8) == 0;
+#pragma unroll
+    for (int j = 0; j < C::TM; ++j) {
+      auto* rbase = region + f_row * C::kEpiRowBytes + f_group * 8;
+#pragma unroll
+      for (int i = 0; i < C::TN; ++i) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t bits = (s2[i][e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+          v[e] = (float(acc[j][i][e]) * rs[j]) * bf16_to_f32(bits);
+        }
+        *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(rbase + i * 32) =
+            u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+      }
+      // One wave's LDS operations complete in order; the wait only orders the reads
+      // after every lane's writes for the compiler.
+      __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int it = 0; it < (16 * kChunks + 63) / 64; ++it) {
+        const int q = it * 64 + lane;
+        if (q >= 16 * kChunks) break;
+        const int row = q / kChunks, chunk = q % kChunks;
+        const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+            region + row * C::kEpiRowBytes + chunk * 16);
+        const int grow = row0 + j * 16 + row, gcol = col0 + chunk * 8;
+        uint16_t* dst = out + int64_t(grow) * n + gcol;
+        if (full) {
+          *reinterpret_cast<u32x4*>(dst) = v;
+        } else if (grow < m) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (gcol + e < n) dst[e] = uint16_t(v[e >> 1] >> (16 * (e & 1)));
+        }
+      }
+      // The next row block's writes reuse the region after these reads.
+      __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+      __builtin_amdgcn_wave_barrier();
+    }
+    if (more) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the next tile's first copies landed
+      barrier_fenced();                          // every wave's, and A slot 1 is free
+    }
+    stamp(kStampTileEnd);
+  }
+  if constexpr (kStamps > 0) {
+    const int64_t clock1 = __builtin_amdgcn_s_memtime();
+    const int64_t wall1 = __builtin_amdgcn_s_memrealtime();
+    int64_t* record = stamps + int64_t(blockIdx.x) * 24;
+    if (lane == 0 && wave == 0) {
+      record[0] = clock0;
+      record[1] = clock1;
+      record[2] = wall0;
+      record[3] = wall1;
+    }
+    if (lane == 0 && wave == C::WM) {
+      record[20] = clock0;
+      record[21] = clock1;
+      record[22] = 0;
+      record[23] = 0;
+    }
+    if (lane == 0 && (wave == 0 || wave == C::WM)) {
+#pragma unroll
+      for (int i = 0; i < kStampKinds; ++i) record[4 + (wave / C::WM) * kStampKinds + i] = phase[i];
+    }
+  }
+}
+
+}  // namespace
+}  // namespace ci8

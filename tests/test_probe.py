@@ -41,3 +41,24 @@ def test_stream_probes_export_and_reject_bad_arguments():
         assert fn(buf, 1000, buf, 256, None) != 0           # not a multiple of 16 bytes
         assert fn(buf, 0, buf, 256, None) != 0              # empty
         assert fn(buf, 1024, buf, 0, None) != 0             # no workgroups
+
+
+def test_stamped_gemm_rejects_bad_arguments_before_any_hip_call():
+    """The clock-stamped persistent GEMM (bench.py --phase-profile) validates pointers,
+    alignment, shape and mode before it queries the device."""
+    lib = ctypes.CDLL(str(PROBE_PATH))
+    fn = lib.ci8probe_pp_gemm_stamped
+    fn.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 4 + [ctypes.c_void_p] * 2
+    p = ctypes.c_void_p(0x10000)
+    ok = dict(a=p, w=p, sa=p, sw=p, out=p, m=256, n=224, k=128, mode=1, stamps=p)
+
+    def call(**change):
+        args = {**ok, **change}
+        return fn(args["a"], args["w"], args["sa"], args["sw"], args["out"], args["m"],
+                  args["n"], args["k"], args["mode"], args["stamps"], None)
+
+    assert call(a=None) != 0 and call(stamps=None) != 0
+    assert call(mode=0) != 0 and call(mode=3) != 0
+    assert call(n=226) != 0 and call(k=100) != 0 and call(m=0) != 0
+    assert call(a=ctypes.c_void_p(0x10008)) != 0      # A not 16-byte aligned
+    assert call(sw=ctypes.c_void_p(0x10004)) != 0     # channel scales not 8-byte aligned
