@@ -371,8 +371,10 @@ PP_BM, PP_BN, PP_BK = 256, 224, 128
 PP_STAGE_FLOOR_CYCLES = 2 * 4 * 7 * 2 * 16
 PHASES = ["memory phase (fragment reads + copies issued)", "wait for W(t+1) (group 1)",
           "barrier 1", "compute phase (56 MFMAs)", "wait for A(t+1) (group 0)", "barrier 2"]
-TILE_PHASES = ["tile start (scale loads, zeroing, group 1's offset barrier)",
-               "tile end (drain barriers, next tile's first copies, epilogue)"]
+TILE_PHASES = ["tile start (scale copies, zeroing, group 1's offset barrier)",
+               "drain (the ping-pong's last phase, barriers)",
+               "epilogue (scaling, BF16 packing, LDS-staged stores)",
+               "tile switch (wait for the next tile's first copies and this tile's stores, barrier)"]
 
 
 def phase_profile(torch, ops, xs, ws, sw, codes, sa, out, reps: int = 6) -> tuple[str, bool]:
@@ -380,7 +382,9 @@ def phase_profile(torch, ops, xs, ws, sw, codes, sa, out, reps: int = 6) -> tupl
     library's kernel source with clock stamps). Mode 1 stamps only each workgroup's start
     and end (shader clock and the 100 MHz wall clock); mode 2 also sums each wave's cycles
     per phase kind for wave 0 (copies A) and wave 4 (copies W). Launches rotate over the
-    bench's input copies; both modes' last output must equal fused_channel_mm's bit for bit."""
+    bench's input copies; both modes' last output must equal fused_channel_mm's bit for bit.
+    Record layout (pp_gemm_kernel): wave 0's clock start, end, wall start, end; the
+    `kinds` sums of wave 0, then of wave 4; wave 4's clock start and end."""
     import ctypes
 
     lib = ctypes.CDLL(str(REPO / "consumer-int8-kernels_amd" / "consumer_int8" / "libci8_probe.so"))
@@ -389,13 +393,15 @@ def phase_profile(torch, ops, xs, ws, sw, codes, sa, out, reps: int = 6) -> tupl
     shader_khz, wall_khz = ctypes.c_int(0), ctypes.c_int(0)
     assert lib.ci8probe_clock_rates(ctypes.byref(shader_khz), ctypes.byref(wall_khz)) == 0
     grid = lib.ci8probe_pp_grid(M, N)
+    words, kinds = lib.ci8probe_pp_stamp_words(), lib.ci8probe_pp_stamp_kinds()
+    assert kinds == len(PHASES) + len(TILE_PHASES) and words >= 6 + 2 * kinds
     tiles = -(-M // PP_BM) * -(-N // PP_BN)
     ns = -(-K // PP_BK)
     my_tiles = torch.tensor([(tiles - b + grid - 1) // grid for b in range(grid)], dtype=torch.float64)
     ops.quantize_rows(xs[0], codes[0], sa)
     want = torch.empty_like(out)
     ops.fused_channel_mm(codes[0], ws[0], sa, sw, want, 0)
-    record = torch.zeros(reps, grid * 24, dtype=torch.int64, device="cuda")
+    record = torch.zeros(reps, grid * words, dtype=torch.int64, device="cuda")
 
     def stamped(i, mode, rec):
         j = i % len(ws)
@@ -424,7 +430,7 @@ def phase_profile(torch, ops, xs, ws, sw, codes, sa, out, reps: int = 6) -> tupl
     recs, exact = {}, True
     for mode in (1, 2):
         kernel_us[mode] = timed(lambda i, r, mode=mode: stamped(i, mode, record[r]))
-        recs[mode] = record.view(reps, grid, 24).cpu().double()
+        recs[mode] = record.view(reps, grid, words).cpu().double()
         out.zero_()
         stamped(0, mode, record[0])
         torch.cuda.synchronize()
@@ -437,10 +443,11 @@ def phase_profile(torch, ops, xs, ws, sw, codes, sa, out, reps: int = 6) -> tupl
     per_tile = float((cycles / my_tiles).mean())
     floor_tile = ns * PP_STAGE_FLOOR_CYCLES
     r2 = recs[2]
-    per_stage = [(r2[:, :, 4 + 8 * g:10 + 8 * g] / (my_tiles * ns)[:, None]).mean(dim=(0, 1))
-                 for g in (0, 1)]
-    per_tile2 = [(r2[:, :, 10 + 8 * g:12 + 8 * g] / my_tiles[:, None]).mean(dim=(0, 1))
-                 for g in (0, 1)]
+    loop = len(PHASES)
+    per_stage = [(r2[:, :, 4 + kinds * g:4 + kinds * g + loop] / (my_tiles * ns)[:, None])
+                 .mean(dim=(0, 1)) for g in (0, 1)]
+    per_tile2 = [(r2[:, :, 4 + kinds * g + loop:4 + kinds * (g + 1)] / my_tiles[:, None])
+                 .mean(dim=(0, 1)) for g in (0, 1)]
     lines = [
         f"configs[2] M={M} K={K} N={N}: {tiles} tiles of {PP_BM}x{PP_BN} on {grid} workgroups "
         f"({tiles / grid:.3f} rounds), {ns} K stages of {PP_BK} per tile.",

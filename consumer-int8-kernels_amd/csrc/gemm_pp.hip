@@ -8,11 +8,16 @@
 // per four bytes after each W fragment read.
 //
 // Persistent: one workgroup of eight waves per CU walks the 256 (m) x 224 (n) output
-// tiles b, b + grid, ... (grid = CU count). Between two tiles, the next tile's first
-// copies (A(0), W(0), W(1)) go out before this tile's epilogue, which then runs through
-// the one ring slot those copies do not use, so the operand latency of a tile start
-// hides behind the previous tile's stores (measured on MI355X at configs[2]: 281.6 ->
-// 277.7 us together with issuing no copies past a tile's last stage).
+// tiles b, b + grid, ... (grid = CU count). The copy stream runs on across tiles: the K
+// stages g = r * ns + t of the whole launch (tile r, stage t) use ring slots g % 2 (A)
+// and g % 3 (W), and a tile's last stages copy the next tile's first stages just as they
+// copy their own, so the tile switch issues no copies and the address unit is free for
+// the epilogue's stores (measured on MI355X at configs[2]: 105 K against 108 K cycles
+// per tile, 255.6-257.4 against 259.6-261.0 us, identical outputs). The epilogue runs
+// through the A slot of the tile's last stage, which the next tile's first copies do not
+// use. The tile's row and channel scales are copied into LDS at the tile start and read
+// back by the epilogue, so they hold no registers through the K loop. With one K stage
+// (K <= 128) the next tile's first copies go out at the tile switch instead.
 //
 // Within a tile, wave w owns rows 64 * (w % 4)
 // and columns 112 * (w / 4) of the tile, as 4 x 7 blocks of v_mfma_i32_16x16x64_i8
@@ -43,6 +48,8 @@
 //   W: three 28 KB slots. W(t + 2) is copied in phase 2t + 1 into the slot of W(t - 1),
 //      read in phases 2t - 2 and 2t - 1; group 1 waits for W(t + 1) at the end of phase
 //      2t + 1.
+// In a tile's last stage group 0 copies the next tile's A(0), and in its last two group
+// 1 copies the next tile's W(0) and W(1); those are waited for at the tile switch.
 // A W wave has 7 copies per stage against an A wave's 8; its eighth reads nothing into a
 // junk KiB, which keeps the copy sequence identical and branch-free.
 //

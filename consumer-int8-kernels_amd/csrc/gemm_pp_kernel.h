@@ -31,7 +31,12 @@ struct PPConfig {
   // distinct banks).
   static constexpr int kEpiRowBytes = (BN / 2) * 2 + 16;
   static constexpr int kEpiPassBytes = 16 * kEpiRowBytes;  // one 16-row block per wave
-  static constexpr int kLdsBytes = kRingBytes;
+  // The tile's row scales (256 FP32) and channel scales (224 BF16, copied as 256), copied
+  // into LDS at the tile start (waves 0-3 their own 64 rows' scales, waves 4 and 5 128
+  // channels each, 4 bytes a lane) and read back by the epilogue, so they take no
+  // registers through the K loop.
+  static constexpr int kScaleBase = kRingBytes;
+  static constexpr int kLdsBytes = kRingBytes + 4 * BM + 2 * 256;
   // m tiles per raster group: each XCD's 32 tiles of a round then cover 4 m x 8 n
   // tiles (measured on MI355X against 2, 8 and 16: configs[2] 277-278 against 280-286
   // us at 8; configs[3] 1,108-1,110 against 1,152-1,154 us).
@@ -56,15 +61,17 @@ __device__ __forceinline__ void barrier_fenced() {
 // kStamps (a measurement build only; the library uses 0): 1 records each workgroup's
 // shader-clock and wall-clock times at start and end, 2 also sums, per wave, the cycles of
 // each phase kind (PhaseStamp) and records those of waves 0 and 4 (one of each group).
-// Layout of `stamps`, 24 values per workgroup: wave 0's clock start, clock end, wall
-// start and wall end, the 8 sums of wave 0, the 8 of wave 4, then wave 4's clock start
-// and end and two zeros. Each wave's sums add up to its own clock end minus its clock
-// start. Reading s_memtime waits for the read, so mode 2 runs slower than the kernel it
-// describes.
+// Layout of `stamps`, kStampWords values per workgroup: wave 0's clock start, clock end,
+// wall start and wall end; the kStampKinds sums of wave 0, then those of wave 4; wave 4's
+// clock start and end; the rest is not written. Each wave's sums add up to its own clock
+// end minus its clock start. Reading s_memtime waits for the read, so mode 2 runs slower
+// than the kernel it describes.
 enum PhaseStamp {
   kStampMemory, kStampWaitW, kStampBarrier1, kStampCompute, kStampWaitA, kStampBarrier2,
-  kStampTileStart, kStampTileEnd, kStampKinds
+  kStampTileStart, kStampDrain, kStampEpilogue, kStampTileEnd, kStampKinds
 };
+constexpr int kStampWords = 32;
+static_assert(6 + 2 * kStampKinds <= kStampWords, "stamp record");
 
 template <bool kExactK, WeightCode kCode, int kStamps = 0>
 __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
@@ -105,6 +112,8 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
   const auto w_rsrc = make_rsrc(w, uint32_t(n) * uint32_t(k));
   const auto c_rsrc = copies_a ? a_rsrc : w_rsrc;
   const int ns = (k + C::BK - 1) / C::BK;
+  const auto sa_rsrc = make_rsrc(sa, uint32_t(m) * 4u);
+  const auto sw_rsrc = make_rsrc(sw, uint32_t(n) * 2u);
 
   // Copy i of a wave brings block b = 4i + wave % 4 of its operand's stage (8 rows x 128
   // bytes): lane -> row 8b + lane / 8, LDS chunk slot lane % 8 holding logical chunk
@@ -135,14 +144,15 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
     __builtin_amdgcn_raw_ptr_buffer_load_lds(c_rsrc, reinterpret_cast<lds_void*>(lds + to), 16,
                                              off, k0, 0, 0);
   };
-  // A tile's first copies: A(0) (group 0) into A slot 0, W(0) and W(1) (group 1) into
-  // W slots 0 and 1.
-  auto first_copies = [&] __device__() __attribute__((always_inline)) {
+  // A tile's first copies, where the previous tile's last stages did not issue them (the
+  // launch's first tile, and every tile when ns == 1): A(0) (group 0) into A slot a_slot,
+  // W(0) and W(1) (group 1) into W slots w_slot0 and w_slot1.
+  auto first_copies = [&] __device__(int a_slot, int w_slot0, int w_slot1) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < C::kCopies; ++i) copy(c_dst0, 0, i);
+    for (int i = 0; i < C::kCopies; ++i) copy(c_dst0 + (copies_a ? a_slot : w_slot0) * c_stride, 0, i);
     if (!copies_a && 1 < ns) {
 #pragma unroll
-      for (int i = 0; i < C::kCopies; ++i) copy(c_dst0 + c_stride, 1, i);
+      for (int i = 0; i < C::kCopies; ++i) copy(c_dst0 + w_slot1 * c_stride, 1, i);
     }
   };
 
@@ -217,51 +227,60 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
   int m0, n0;
   tile_of(int(blockIdx.x), m0, n0);
   set_copy_tile(m0, n0);
-  first_copies();
+  first_copies(0, 0, 1);
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  // Ring slots run on across tiles: stage g of the launch's stream (tile r, K stage t,
+  // g = r * ns + t) uses A slot g % 2 and W slot g % 3. With ns >= 2 the next tile's
+  // first stages are copied by the current tile's last stages like any other stage.
+  int a_slot = 0;   // g % 2
+  int w_slot = 0;   // g % 3
+  int cw_slot = 2;  // (g + 2) % 3
+  const bool stream_ok = ns >= 2;
   barrier_fenced();
 
   for (int r = 0; r < my_tiles; ++r) {
-    // This tile's row and channel scales, loaded now (older than any copy of the tile,
+    // This tile's row and channel scales go to LDS now (older than any copy of the tile,
     // so the waits of the K loop cover them).
-    float rs[C::TM];
-    u32x2 s2[C::TN];
-    {
-      const int row0 = m0 + wm * 64, col0 = n0 + group * 112;
-#pragma unroll
-      for (int j = 0; j < C::TM; ++j) {
-        const int row = row0 + j * 16 + f_row;
-        rs[j] = row < m ? sa[row] : 0.f;
-      }
-#pragma unroll
-      for (int i = 0; i < C::TN; ++i) {
-        const int col = col0 + i * 16 + f_group * 4;
-        s2[i] = col < n ? *reinterpret_cast<const u32x2*>(sw + col) : u32x2{0, 0};
-      }
+    if (wave < C::WM + 2) {  // uniform over the wave
+      const bool rows = wave < C::WM;
+      const int part = rows ? wave : wave - C::WM;
+      const uint32_t off = rows ? uint32_t(m0 + part * 64) * 4u + uint32_t(lane) * 4u
+                                : uint32_t(n0 + part * 128) * 2u + uint32_t(lane) * 4u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rows ? sa_rsrc : sw_rsrc,
+          reinterpret_cast<lds_void*>(lds + C::kScaleBase + (rows ? 0 : 4 * C::BM) + part * 256),
+          4, off, 0, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < C::TM; ++j)
 #pragma unroll
       for (int i = 0; i < C::TN; ++i) acc[j][i] = i32x4{0, 0, 0, 0};
 
-    // Stage t: group 0 copies A(t + 1) (into A slot (t + 1) % 2), group 1 W(t + 2) (into
-    // W slot (t + 2) % 3). The last stages, with nothing left to copy, issue no copies,
-    // and group 1 then waits for all of its copies instead of all but the newest stage's.
-    int w_slot = 0;   // t % 3
-    int cw_slot = 2;  // (t + 2) % 3
+    const int tile_m0 = m0, tile_n0 = n0;
+    const bool more = r + 1 < my_tiles;
     const int lead = copies_a ? 1 : 2;
     if (group == 1) barrier_fenced();  // phase 0 is group 0's first memory phase
     stamp(kStampTileStart);
     for (int t = 0; t < ns; ++t) {
-      const int copy_t = t + lead;
-      const int dst = c_dst0 + (copies_a ? (t + 1) & 1 : cw_slot) * c_stride;
-      if (copy_t < ns) {  // uniform over the wave
-        memory(t & 1, w_slot, dst, copy_t, std::true_type{});
+      int copy_t = t + lead;
+      const bool next_tile = copy_t >= ns;
+      if (next_tile && more && stream_ok) {
+        if (copy_t == ns) {  // this group's first copy of the next tile
+          tile_of(int(blockIdx.x) + (r + 1) * grid, m0, n0);
+          set_copy_tile(m0, n0);
+        }
+        copy_t -= ns;
+      }
+      const bool copies = !next_tile || (more && stream_ok);
+      const int dst = c_dst0 + (copies_a ? a_slot ^ 1 : cw_slot) * c_stride;
+      if (copies) {  // uniform over the wave
+        memory(a_slot, w_slot, dst, copy_t, std::true_type{});
         stamp(kStampMemory);
-        // Group 1: W(t + 1) landed (W(t + 2), just issued, may be in flight).
-        if (group == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(C::kCopies));
+        // Group 1: W(t + 1) landed (W(t + 2), just issued, may be in flight). In the last
+        // stage nothing of this tile is left to wait for.
+        if (group == 1 && t + 1 < ns) __builtin_amdgcn_s_waitcnt(vmcnt_imm(C::kCopies));
       } else {
-        memory(t & 1, w_slot, dst, copy_t, std::false_type{});
+        memory(a_slot, w_slot, dst, copy_t, std::false_type{});
         stamp(kStampMemory);
         if (group == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
       }
@@ -270,40 +289,45 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
       stamp(kStampBarrier1);
       compute();
       stamp(kStampCompute);
-      // Group 0: A(t + 1), issued in the memory phase, landed.
-      if (group == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      // Group 0: A(t + 1), issued in the memory phase, landed (in the last stage, the next
+      // tile's A(0) is waited for at the tile switch).
+      if (group == 0 && (t + 1 < ns || !stream_ok)) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
       stamp(kStampWaitA);
       barrier_fenced();
       stamp(kStampBarrier2);
+      a_slot ^= 1;
       w_slot = w_slot == 2 ? 0 : w_slot + 1;
       cw_slot = cw_slot == 2 ? 0 : cw_slot + 1;
     }
     if (group == 0) barrier_fenced();  // phase 2 ns: group 1's last compute phase
     barrier_fenced();                  // every wave is past its last fragment reads
-
-    // The next tile's first copies go out now, into A slot 0 and W slots 0 and 1, and
-    // land while this tile's results are stored through A slot 1. Every load of this
-    // tile has landed by now (each wave waited for its last copies); the explicit wait
-    // says so to the compiler, which otherwise waits for those first copies before the
-    // epilogue's first use of the scales loaded at the tile start.
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    const int tile_m0 = m0, tile_n0 = n0;
-    const bool more = r + 1 < my_tiles;
-    if (more) {
+    stamp(kStampDrain);
+    if (more && !stream_ok) {
       tile_of(int(blockIdx.x) + (r + 1) * grid, m0, n0);
       set_copy_tile(m0, n0);
-      first_copies();
+      first_copies(a_slot, w_slot, w_slot == 2 ? 0 : w_slot + 1);
     }
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
 
     // Epilogue through LDS, 16 rows of the wave's 64 at a time: the 16 x 112 BF16
-    // results of row block j go to the wave's 3840-byte region of A slot 1 in the MFMA
-    // layout and come back as 16-byte row chunks, so each store instruction writes whole
-    // 224-byte row pieces (14 lanes per row).
+    // results of row block j go to the wave's 3840-byte region of the A slot the tile's
+    // last stage used (the next tile's A(0) is in the other) in the MFMA layout and come
+    // back as 16-byte row chunks, so each store instruction writes whole 224-byte row
+    // pieces (14 lanes per row).
     const int row0 = tile_m0 + wm * 64;
     const int col0 = tile_n0 + group * 112;
-    auto* region = lds + C::kAStage + wave * C::kEpiPassBytes;
+    auto* region = lds + (a_slot ^ 1) * C::kAStage + wave * C::kEpiPassBytes;
+    float rs[C::TM];
+    u32x2 s2[C::TN];
+#pragma unroll
+    for (int j = 0; j < C::TM; ++j)
+      rs[j] = *reinterpret_cast<const __attribute__((address_space(3))) float*>(
+          lds + C::kScaleBase + (wm * 64 + j * 16 + f_row) * 4);
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i)
+      s2[i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>(
+          lds + C::kScaleBase + 4 * C::BM + (group * 112 + i * 16 + f_group * 4) * 2);
     constexpr int kChunks = 112 / 8;  // 16-byte chunks per output row piece
     const bool full = out16 && row0 + 64 <= m && col0 + 112 <= n && (n % 8) == 0;
 #pragma unroll
@@ -345,16 +369,17 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
       __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
       __builtin_amdgcn_wave_barrier();
     }
+    stamp(kStampEpilogue);
     if (more) {
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the next tile's first copies landed
-      barrier_fenced();                          // every wave's, and A slot 1 is free
+      barrier_fenced();  // every wave's, and the epilogue's LDS (A slot, scales) is free
     }
     stamp(kStampTileEnd);
   }
   if constexpr (kStamps > 0) {
     const int64_t clock1 = __builtin_amdgcn_s_memtime();
     const int64_t wall1 = __builtin_amdgcn_s_memrealtime();
-    int64_t* record = stamps + int64_t(blockIdx.x) * 24;
+    int64_t* record = stamps + int64_t(blockIdx.x) * kStampWords;
     if (lane == 0 && wave == 0) {
       record[0] = clock0;
       record[1] = clock1;
@@ -362,10 +387,8 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
       record[3] = wall1;
     }
     if (lane == 0 && wave == C::WM) {
-      record[20] = clock0;
-      record[21] = clock1;
-      record[22] = 0;
-      record[23] = 0;
+      record[4 + 2 * kStampKinds] = clock0;
+      record[5 + 2 * kStampKinds] = clock1;
     }
     if (lane == 0 && (wave == 0 || wave == C::WM)) {
 #pragma unroll

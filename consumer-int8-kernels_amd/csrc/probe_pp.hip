@@ -5,11 +5,11 @@
 
 extern "C" {
 
-// fused_channel_mm with signed weights through the persistent kernel, recording 24
-// int64 values per workgroup into `stamps` (pp_gemm_kernel's stamp layout): mode 1 the
-// shader-clock and wall-clock start and end times, mode 2 also per-phase cycle sums.
-// `stamps` holds at least ci8probe_pp_grid(m, n) * 24 values. Same requirements as
-// fused_channel_mm's persistent path: a, w 16-byte aligned, sw 8-byte aligned, n % 4 == 0.
+// The stamp record: int64 values per workgroup, and phase kinds (pp_gemm_kernel's layout).
+int ci8probe_pp_stamp_words() { return ci8::kStampWords; }
+int ci8probe_pp_stamp_kinds() { return ci8::kStampKinds; }
+
+// Workgroups of the persistent kernel's launch at m x n (one per CU, at most one per tile).
 int ci8probe_pp_grid(int m, int n) {
   using C = ci8::PPConfig;
   const int tiles = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
@@ -17,6 +17,12 @@ int ci8probe_pp_grid(int m, int n) {
   return cus > 0 && cus < tiles ? cus : tiles;
 }
 
+// fused_channel_mm with signed weights through the persistent kernel, recording
+// ci8probe_pp_stamp_words() values per workgroup into `stamps`: mode 1 the shader-clock
+// and wall-clock start and end times, mode 2 also the per-phase cycle sums. `stamps` holds
+// at least ci8probe_pp_grid(m, n) * ci8probe_pp_stamp_words() values, zeroed by the
+// caller. Same requirements as fused_channel_mm's persistent path: a, w 16-byte aligned,
+// sw 8-byte aligned, n % 4 == 0.
 int ci8probe_pp_gemm_stamped(const int8_t* a, const int8_t* w, const float* sa, const void* sw,
                              void* out, int m, int n, int k, int mode, int64_t* stamps,
                              void* stream) {

@@ -267,6 +267,41 @@ def test_wide_tiles_where_they_fill_the_rounds(ops, biased):
     full_size_check(a_np, w_signed, sa_np, sw_np, acc, out_bits, samples=8)
 
 
+@pytest.mark.parametrize("m,n,k,biased", [
+    (2048, 17408, 128, False),   # one K stage: the next tile's copies go out at the switch
+    (2048, 17408, 256, True),    # two stages: group 1 copies the next tile from stage 0
+    (2048, 17408, 384, False),   # an odd stage count: ring slots alternate across tiles
+    (3000, 9000, 1056, True),    # K tail, ragged M and N tiles
+])
+def test_persistent_tile_switches(ops, m, n, k, biased):
+    """Shapes where the persistent kernel runs two or more tiles per workgroup, so each
+    workgroup's copy stream runs on from one tile's last stages into the next tile's first
+    (ring slots numbered over the whole launch). The output equals the 128 x 128 tiling's
+    (schedule 1) and the workspace kernel's, whose exact INT32 accumulators are checked
+    against the oracle through checksums and sampled rows and columns."""
+    rng = np.random.default_rng(m + n + k + biased)
+    a_np, w_np, sa_np, sw_np = gemm_inputs(rng, m, n, k, biased=biased)
+    w_signed = O.debias(w_np) if biased else w_np
+    a, sa, sw, ws_dev = to_dev(a_np), to_dev(sa_np), to_dev(sw_np), to_dev(w_signed)
+    out, buf = with_guard((m, n), torch.bfloat16, float("nan"))
+    print(f"persistent tile switches m={m} n={n} k={k} biased={biased}", flush=True)
+    if biased:
+        ops.channel_mm(a, to_dev(w_np), sa, sw, out)
+    else:
+        ops.fused_channel_mm(a, ws_dev, sa, sw, out, 0)
+    ref = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    ops.fused_channel_mm(a, ws_dev, sa, sw, ref, 1)
+    acc = torch.empty(m, n, device="cuda", dtype=torch.int32)
+    out2 = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    ops.cutlass_channel_mm(a, ws_dev, sa, sw, acc, out2)
+    torch.cuda.synchronize()
+    out_bits = bf16_bits(out)
+    assert guard_intact(buf, float("nan"))
+    assert np.array_equal(out_bits, bf16_bits(ref))
+    assert np.array_equal(out_bits, bf16_bits(out2))
+    full_size_check(a_np, w_signed, sa_np, sw_np, acc, out_bits, samples=8)
+
+
 def test_c_abi_fused_matches_oracle(ops, lib):
     from consumer_int8 import _abi
 

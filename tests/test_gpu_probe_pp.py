@@ -19,8 +19,6 @@ from tests.helpers import bf16_bits, to_dev
 
 pytestmark = pytest.mark.gpu
 
-STAMP_WORDS = 24  # per workgroup: wave 0's 4 times, 8 phase sums each for waves 0 and 4,
-                  # wave 4's clock start and end, 2 zeros
 
 
 def probe():
@@ -30,7 +28,8 @@ def probe():
     return lib
 
 
-@pytest.mark.parametrize("m,n,k", [(1024, 896, 640), (1100, 900, 608), (2048, 4096, 1024)])
+@pytest.mark.parametrize("m,n,k", [(1024, 896, 640), (1100, 900, 608), (2048, 4096, 1024),
+                                   (2048, 4096, 128), (1300, 3000, 256)])
 @pytest.mark.parametrize("mode", [1, 2])
 def test_stamped_kernel_matches_fused_channel_mm(ops, m, n, k, mode):
     rng = np.random.default_rng(m + n + k + mode)
@@ -42,9 +41,11 @@ def test_stamped_kernel_matches_fused_channel_mm(ops, m, n, k, mode):
     ops.fused_channel_mm(a, w, sa, sw, want, 0)
     lib = probe()
     grid = lib.ci8probe_pp_grid(m, n)
+    words, kinds = lib.ci8probe_pp_stamp_words(), lib.ci8probe_pp_stamp_kinds()
+    assert words >= 6 + 2 * kinds
     tiles = -(-m // 256) * -(-n // 224)
     assert 0 < grid <= tiles
-    stamps = torch.zeros(grid * STAMP_WORDS, dtype=torch.int64, device="cuda")
+    stamps = torch.zeros(grid * words, dtype=torch.int64, device="cuda")
     out = torch.full((m, n), float("nan"), device="cuda", dtype=torch.bfloat16)
     stream = torch.cuda.current_stream().cuda_stream
     assert lib.ci8probe_pp_gemm_stamped(a.data_ptr(), w.data_ptr(), sa.data_ptr(), sw.data_ptr(),
@@ -52,10 +53,11 @@ def test_stamped_kernel_matches_fused_channel_mm(ops, m, n, k, mode):
                                         stream) == 0
     torch.cuda.synchronize()
     assert np.array_equal(bf16_bits(out), bf16_bits(want))
-    rec = stamps.view(grid, STAMP_WORDS).cpu()
+    rec = stamps.view(grid, words).cpu()
+    start4, end4 = 4 + 2 * kinds, 5 + 2 * kinds
     assert bool((rec[:, 1] > rec[:, 0]).all()) and bool((rec[:, 3] > rec[:, 2]).all())
-    assert bool((rec[:, 21] > rec[:, 20]).all()) and bool((rec[:, 22:] == 0).all())
-    phases = rec[:, 4:20]
+    assert bool((rec[:, end4] > rec[:, start4]).all()) and bool((rec[:, 6 + 2 * kinds:] == 0).all())
+    phases = rec[:, 4:4 + 2 * kinds]
     if mode == 1:
         assert bool((phases == 0).all())
     else:
@@ -63,8 +65,8 @@ def test_stamped_kernel_matches_fused_channel_mm(ops, m, n, k, mode):
         # a wave's sums add up to its own start-to-end time less the few cycles between
         # its last stamp and its end-time read.
         assert bool((phases >= 0).all())
-        assert bool((rec[:, 4 + 3] > 0).all()) and bool((rec[:, 12 + 3] > 0).all())
-        for first, start, end in ((4, 0, 1), (12, 20, 21)):
-            total = rec[:, first:first + 8].sum(dim=1)
+        assert bool((rec[:, 4 + 3] > 0).all()) and bool((rec[:, 4 + kinds + 3] > 0).all())
+        for first, start, end in ((4, 0, 1), (4 + kinds, start4, end4)):
+            total = rec[:, first:first + kinds].sum(dim=1)
             span = rec[:, end] - rec[:, start]
             assert bool((total <= span).all() and (total >= span - 500).all()), (first, total, span)

@@ -13,11 +13,14 @@ PROBE_PATH = PKG / "consumer_int8" / "libci8_probe.so"
 def test_probe_library_exports():
     lib = ctypes.CDLL(str(PROBE_PATH))
     for name in ("ci8probe_mfma_loop", "ci8probe_clock_rates", "ci8probe_mfma_per_round",
-                 "ci8probe_ops_per_mfma"):
+                 "ci8probe_ops_per_mfma", "ci8probe_pp_gemm_stamped", "ci8probe_pp_grid",
+                 "ci8probe_pp_stamp_words", "ci8probe_pp_stamp_kinds"):
         assert hasattr(lib, name), name
     lib.ci8probe_ops_per_mfma.restype = ctypes.c_int64
     assert lib.ci8probe_mfma_per_round() == 32
     assert lib.ci8probe_ops_per_mfma() == 16 * 16 * 64 * 2
+    # The stamp record holds wave 0's four times, two waves' phase sums and wave 4's two.
+    assert lib.ci8probe_pp_stamp_words() >= 6 + 2 * lib.ci8probe_pp_stamp_kinds()
 
 
 def test_probe_rejects_bad_launches_before_any_hip_call():
