@@ -496,7 +496,8 @@ __global__ void __launch_bounds__(C::kThreads, C::kWavesPerEU) channel_gemv_pers
 // products, so at each row the loads issued after its own are the next row's kC + 1
 // (codes and scale), and vmcnt(kC + 1) means row r has landed. A lane dequantizes its
 // 16 codes exactly as the MFMA kernels do (bf16_rn(code * scale), packed in pairs) and
-// feeds them with x to v_dot2_f32_bf16; the 64 lane sums meet by a butterfly, in FP32.
+// feeds them with x to v_dot2_f32_bf16; the 64 lane sums are added in FP32 (DPP within
+// rows of 16 lanes, then the four row sums).
 // Rows past N load nothing (range-checked offsets) and store nothing. The weight loads are
 // nontemporal: every byte is read once (measured on MI355X at K = 5120, N = 17408: 17.0
 // against 17.9 us with plain loads, identical outputs; the balanced-span kernel below
@@ -509,6 +510,27 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
                                          __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// The sum of a float over the 64 lanes, in lane 0 (other lanes hold partial sums): DPP
+// adds within each row of 16 lanes (quad swaps, then the half-row and row mirrors), then
+// the four row sums read out and added. Measured on MI355X against a ds_bpermute
+// butterfly (M = 1, identical inputs): 5.48-5.56 against 5.64-5.68 us at N = K = 4096,
+// 14.28-14.40 against 14.90-14.91 us at N = K = 8192, level at K = 5120, N = 17408.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_move(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_to_lane0(float v) {
+  v += dpp_move<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_move<0x141>(v);  // row_half_mirror
+  v += dpp_move<0x140>(v);  // row_mirror: every lane of a row holds the row's sum
+  auto lane_value = [&](int l) __attribute__((always_inline)) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+  };
+  return (lane_value(0) + lane_value(16)) + (lane_value(32) + lane_value(48));
 }
 
 template <int kC>
@@ -568,9 +590,8 @@ __global__ void __launch_bounds__(256) channel_gemv_rows_kernel(
         }
       issue(row + kAhead * stride, s);
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
-      if (lane == 0 && row < n) out[row] = uint16_t(f32_to_bf16(acc));
+      const float total = wave_sum_to_lane0(acc);
+      if (lane == 0 && row < n) out[row] = uint16_t(f32_to_bf16(total));
     }
   }
   waitcnt<vmcnt_imm(0)>();  // drain the trailing (out-of-range) loads before exit
