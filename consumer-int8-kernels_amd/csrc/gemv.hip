@@ -33,7 +33,11 @@
 // and the dot product on the VALU (v_dot2_f32_bf16 on the BF16 products).
 // For K <= 8192 and 2 <= m <= 16, a balanced-span kernel (one 16-wave workgroup per
 // CU over an equal share of the channels, x fragments held in registers, W streamed one
-// block of 16 channels ahead) replaces the kernels below. At m = 1 for longer K
+// block of 16 channels ahead) replaces the kernels below, except where an interleaved
+// quad-block kernel is faster (2 <= m <= 4 with K >= 4096, and 5 <= m <= 8 with K >
+// 5120): it runs the products on the 4x4x4 MFMA over blocks of 4 channels so that each
+// load instruction reads 4 channels x 256 contiguous bytes, and deals the blocks to the
+// CUs round-robin so the chip streams one contiguous window. At m = 1 for longer K
 // while x[0:m, :] fits in 64 KiB of LDS, a second kernel copies all of x into LDS once
 // and then lets every wave stream its W through a rolling window of ten 64-byte blocks
 // with no barriers at all, which removes the per-stage lock-step of the ring. Up to
@@ -755,6 +759,242 @@ hipError_t run_span(const void* x, const int8_t* w, const void* scale, void* out
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------
+// Interleaved quad-block variant (K in [4096, 8192], m <= 8): blocks of 4 channels on
+// v_mfma_f32_4x4x4bf16_1k.
+//
+// The 4x4x4 MFMA computes 16 independent 4x4 products. Lane 4q + i supplies row i of
+// block q of A and lane 4q + j column j of block q of B; the result of block q lands in
+// lane 4q + j, element i. Here A is W (row i = channel i of a 4-channel block) and B is
+// x (column j = batch row 4g + j of batch group g), and the 16 MFMA blocks q take 16
+// disjoint slices of the K range, so one 16-byte load per lane reads 4 channels x 256
+// contiguous bytes. That is a plain weight stream: each instruction fetches whole
+// 128-byte lines, where the 16 x 16 MFMA layout needs 16 channels x 64 bytes. The
+// price is that every output is a sum over the 16 lane blocks, and that m > 4 needs
+// one MFMA per batch group.
+//  * Blocks are dealt to workgroups round-robin: workgroup b takes blocks b, b + grid,
+//    b + 2 grid, ... (one 16-wave workgroup per CU), so at any time the chip reads one
+//    contiguous window of the weights, which measured faster than contiguous per-CU
+//    spans (a load-only copy of this layout streamed the configs[1] weights in 14.7
+//    against 16.2 us with spans), and N = 17408 gives every CU the same 17 blocks.
+//  * Wave r sums K range r (kU units of 64 elements; loads of 16, 8 and 4 bytes per lane
+//    cover 4, 2 and 1 units). Its x operands for that range stay in registers.
+//  * W streams one block ahead: after a load's MFMAs, the wave issues the same load for
+//    its next block, and the next block's channel scale at the start of a block. Loads
+//    retire in issue order, so before load e of block t the loads issued after it are
+//    the rest of block t, the next scale and the first e loads of block t + 1:
+//    vmcnt(kLoads) means it has landed; vmcnt(kLoads + 1) at the start of a block, after
+//    the next scale is issued, means this block's scale has.
+//  * After a block, two DPP row rotations add the four lane blocks of each 16-lane row;
+//    lanes 16R + j (j < 4) then hold the row-R partials of batch row j for the 4
+//    channels and store them to LDS. kBatch blocks of partials fit in 128 KiB, so the
+//    waves meet at a barrier once per kBatch blocks (at N = 17408 only at the end),
+//    where 4 threads per (block, batch row) add the 16 waves' partials of one R each
+//    and a quad DPP reduction adds the four R. The order of every sum is fixed.
+template <int kU_, int kG_>
+struct QuadConfig {
+  static constexpr int kU = kU_;  // 64-element K units per wave
+  static constexpr int kG = kG_;  // batch groups of 4 rows
+  static constexpr int kS = 16;   // waves, one K range each
+  static constexpr int kThreads = 64 * kS;
+  static constexpr int kN4 = kU / 4, kHas2 = (kU % 4) >= 2, kHas1 = kU % 2;
+  static constexpr int kLoads = kN4 + kHas2 + kHas1;  // W loads per block and wave
+  static constexpr int kBatch = 32 / kG;              // blocks of partials in LDS
+  static_assert(kU >= 4 && kU <= 8, "K ranges of 256 to 512 elements");
+  static_assert(kLoads + 1 <= 63, "vmcnt holds 6 bits");
+};
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 mfma4x4_bf16(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                 __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+}
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp_rotate(float x) {  // every lane's source is valid
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, 0xF, 0xF, true));
+}
+
+template <class C>
+__global__ void __launch_bounds__(C::kThreads) channel_gemv_quad_kernel(
+    const uint16_t* __restrict__ x, const int8_t* __restrict__ w,
+    const uint16_t* __restrict__ scale, uint16_t* __restrict__ out, int m, int n, int k) {
+  __shared__ f32x4 partial[C::kBatch][C::kS][C::kG][16];
+  const int nblk = (n + 3) >> 2;
+  const int grid = int(gridDim.x), b0 = int(blockIdx.x);
+  if (b0 >= nblk) return;  // uniform over the workgroup
+  const int nlocal = (nblk - b0 + grid - 1) / grid;
+
+  const int lane = threadIdx.x & 63;
+  const int range = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = lane >> 2, i = lane & 3;
+  const int kc0 = range * C::kU * 64;
+
+  const auto w_rsrc = make_rsrc(w, uint32_t(n) * uint32_t(k));
+  const auto x_rsrc = make_rsrc(x, uint32_t(m) * uint32_t(k) * 2u);
+  const auto s_rsrc = make_rsrc(scale, uint32_t(n) * 2u);
+
+  // First column of this lane's codes in load e (16, 8 or 4 of them).
+  auto col_of = [&](int e) __attribute__((always_inline)) -> int {
+    if (e < C::kN4) return kc0 + 256 * e + 16 * q;
+    if (C::kHas2 && e == C::kN4) return kc0 + 256 * C::kN4 + 8 * q;
+    return kc0 + 256 * C::kN4 + 128 * C::kHas2 + 4 * q;
+  };
+  // K % 16 == 0, so each load is wholly inside or wholly past its row.
+  auto w_offset = [&](int lb, int e) __attribute__((always_inline)) -> uint32_t {
+    const int channel = 4 * (b0 + lb * grid) + i, col = col_of(e);
+    return lb < nlocal && channel < n && col < k
+               ? uint32_t(channel) * uint32_t(k) + uint32_t(col) : kOutOfRange;
+  };
+  auto load_scale = [&](int lb) __attribute__((always_inline)) -> uint32_t {
+    const int channel = 4 * (b0 + lb * grid) + i;
+    return __builtin_amdgcn_raw_buffer_load_b16(
+        s_rsrc, lb < nlocal && channel < n ? uint32_t(channel) * 2u : kOutOfRange, 0, 0);
+  };
+
+  // x operands: xs[g][u] = x[4g + i, the 4 columns lane block q takes of unit u].
+  u32x2 xs[C::kG][C::kU];
+#pragma unroll
+  for (int g = 0; g < C::kG; ++g) {
+    const int row = 4 * g + i;
+#pragma unroll
+    for (int e = 0; e < C::kLoads; ++e) {
+      const int col = col_of(e);
+      const bool valid = row < m && col < k;
+      const uint32_t base = (uint32_t(row) * uint32_t(k) + uint32_t(col)) * 2u;
+      auto load16 = [&](uint32_t extra) __attribute__((always_inline)) {
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             x_rsrc, valid ? base + extra : kOutOfRange, 0, 0));
+      };
+      if (e < C::kN4) {
+        const u32x4 lo = load16(0), hi = load16(16);
+        xs[g][4 * e] = u32x2{lo[0], lo[1]};
+        xs[g][4 * e + 1] = u32x2{lo[2], lo[3]};
+        xs[g][4 * e + 2] = u32x2{hi[0], hi[1]};
+        xs[g][4 * e + 3] = u32x2{hi[2], hi[3]};
+      } else if (C::kHas2 && e == C::kN4) {
+        const u32x4 v = load16(0);
+        xs[g][4 * C::kN4] = u32x2{v[0], v[1]};
+        xs[g][4 * C::kN4 + 1] = u32x2{v[2], v[3]};
+      } else {
+        xs[g][C::kU - 1] = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(x_rsrc, valid ? base : kOutOfRange, 0, 0));
+      }
+    }
+  }
+  uint32_t s_next = load_scale(0);
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 w4[C::kN4];
+  u32x2 w2;
+  uint32_t w1;
+  auto issue = [&](int lb, int e) __attribute__((always_inline)) {
+    if (e < C::kN4)
+      w4[e] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(lb, e), 0, 0));
+    else if (C::kHas2 && e == C::kN4)
+      w2 = __builtin_bit_cast(
+          u32x2, __builtin_amdgcn_raw_buffer_load_b64(w_rsrc, w_offset(lb, e), 0, 0));
+    else
+      w1 = __builtin_amdgcn_raw_buffer_load_b32(w_rsrc, w_offset(lb, e), 0, 0);
+  };
+#pragma unroll
+  for (int e = 0; e < C::kLoads; ++e) {
+    issue(0, e);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // Adds and stores the partials of local blocks [lb0, lb0 + count). Item (block, batch
+  // row, R) adds the 16 ranges' row-R partials (4 channels); the 4 R of an item are the 4
+  // lanes of a quad.
+  auto reduce = [&](int lb0, int count) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+    workgroup_barrier();
+    const int items = count * m * 4;  // <= 512
+    const int item = int(threadIdx.x), r = item & 3, batch = (item >> 2) % m,
+              b = (item >> 2) / m;
+    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (item < items) {
+#pragma unroll
+      for (int v = 0; v < C::kS; ++v) sum += partial[b][v][batch >> 2][4 * r + (batch & 3)];
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      sum[c] += dpp_rotate<0xB1>(sum[c]);  // quad_perm [1, 0, 3, 2]
+      sum[c] += dpp_rotate<0x4E>(sum[c]);  // quad_perm [2, 3, 0, 1]
+    }
+    if (item < items && r == 0) {
+      const int channel = 4 * (b0 + (lb0 + b) * grid);
+      uint16_t* o = out + int64_t(batch) * n + channel;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (channel + c < n) o[c] = uint16_t(f32_to_bf16(sum[c]));
+    }
+    __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+    workgroup_barrier();
+  };
+
+  for (int lb = 0; lb < nlocal; ++lb) {
+    const float sc = bf16_to_f32(s_next);
+    s_next = load_scale(lb + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    waitcnt<vmcnt_imm(C::kLoads + 1)>();  // the scale of block lb has landed
+    f32x4 acc[C::kG];
+#pragma unroll
+    for (int g = 0; g < C::kG; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < C::kLoads; ++e) {
+      waitcnt<vmcnt_imm(C::kLoads)>();  // W(lb, e) has landed
+      auto step = [&](uint32_t word, int unit) __attribute__((always_inline)) {
+        const u32x2 a = dequant4(word, sc);
+#pragma unroll
+        for (int g = 0; g < C::kG; ++g) acc[g] = mfma4x4_bf16(a, xs[g][unit], acc[g]);
+      };
+      if (e < C::kN4) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) step(w4[e][s], 4 * e + s);
+      } else if (C::kHas2 && e == C::kN4) {
+        step(w2[0], 4 * C::kN4);
+        step(w2[1], 4 * C::kN4 + 1);
+      } else {
+        step(w1, C::kU - 1);
+      }
+      issue(lb + 1, e);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int g = 0; g < C::kG; ++g)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        acc[g][c] += dpp_rotate<0x128>(acc[g][c]);  // row_ror:8
+        acc[g][c] += dpp_rotate<0x124>(acc[g][c]);  // row_ror:4
+      }
+    if ((lane & 15) < 4) {
+#pragma unroll
+      for (int g = 0; g < C::kG; ++g)
+        partial[lb % C::kBatch][range][g][(lane >> 4) * 4 + (lane & 3)] = acc[g];
+    }
+    if (lb % C::kBatch == C::kBatch - 1 || lb + 1 == nlocal)  // uniform
+      reduce(lb / C::kBatch * C::kBatch, lb % C::kBatch + 1);
+  }
+  waitcnt<vmcnt_imm(0)>();  // drain the trailing (out-of-range) loads before exit
+}
+
+template <int kU>
+hipError_t run_quad(const void* x, const int8_t* w, const void* scale, void* out, int m, int n,
+                    int k, int cus, hipStream_t stream) {
+  const int grid = min(cus, (n + 3) / 4);
+  auto launch = [&](auto kernel) {
+    kernel<<<grid, 1024, 0, stream>>>(static_cast<const uint16_t*>(x), w,
+                                      static_cast<const uint16_t*>(scale),
+                                      static_cast<uint16_t*>(out), m, n, k);
+    return hipGetLastError();
+  };
+  if (m <= 4) return launch(channel_gemv_quad_kernel<QuadConfig<kU, 1>>);
+  return launch(channel_gemv_quad_kernel<QuadConfig<kU, 2>>);
+}
+
 }  // namespace
 
 hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale, void* out,
@@ -762,6 +1002,21 @@ hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale
   // K <= 8192 and m >= 2: the balanced-span kernel (measured on MI355X at K = 5120, N =
   // 17408: 20.2 - 22.9 us over m = 2 .. 16, against 20.4 - 30.9 us for the kernels below).
   const int cus = device_cu_count();
+  // 2 <= m <= 4 with 4096 <= K <= 8192, and 5 <= m <= 8 with 5120 < K <= 8192: the
+  // interleaved quad-block kernel (measured at K = 5120, N = 17408: 16.3 / 17.1 us at
+  // m = 2 / 4 against 19.6 / 19.9 us for the span kernel; at N = K = 8192, m = 5 .. 8:
+  // 14.3 - 15.5 against 21.0 - 21.4 us). At K = 3072, or m = 5 .. 8 with K <= 5120, or m
+  // > 8, it loses to the span kernel (one MFMA per 4 batch rows); at m = 1 the row
+  // kernel is as fast or faster at N >= 28672.
+  if (cus > 0 && k >= 4096 && k <= 8192 && ((m >= 2 && m <= 4) || (m >= 5 && m <= 8 && k > 5120))) {
+    switch (((k + 63) / 64 + 15) / 16) {
+      case 4: return run_quad<4>(x, w, scale, out, m, n, k, cus, stream);
+      case 5: return run_quad<5>(x, w, scale, out, m, n, k, cus, stream);
+      case 6: return run_quad<6>(x, w, scale, out, m, n, k, cus, stream);
+      case 7: return run_quad<7>(x, w, scale, out, m, n, k, cus, stream);
+      default: return run_quad<8>(x, w, scale, out, m, n, k, cus, stream);
+    }
+  }
   // m = 1, K <= 8192: whole rows on the VALU (measured at K = 5120, N = 17408: 17.9 us
   // against 21.2 us for the resident MFMA kernel under the same C-side launch loop).
   if (m == 1 && cus > 0 && k <= 8192) {

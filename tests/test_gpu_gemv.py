@@ -81,6 +81,25 @@ def test_balanced_spans(ops, m, n, k):
     check_gemv(bf16_bits(out), x_bits, w, s_bits)
 
 
+@pytest.mark.parametrize("m,n,k", [(2, 4096, 4096), (3, 1001, 4112), (4, 33000, 4096),
+                                   (5, 20002, 6144), (7, 3001, 7168), (8, 4099, 8192),
+                                   (6, 517, 8176), (2, 17408, 5120)])
+def test_quad_block_kernel(ops, m, n, k):
+    """2 <= m <= 4 with 4096 <= K <= 8192, and 5 <= m <= 8 with 5120 < K <= 8192, run the
+    interleaved 4-channel-block kernel: every K range length (4 to 8 units of 64), one
+    and two batch groups, a ragged last K range (4112, 8176), N not a multiple of 4,
+    fewer blocks than CUs, and more blocks per CU than one partial-sum batch holds (N =
+    33000 at one batch group, N = 20002 at two), so the waves also meet mid-way."""
+    rng = np.random.default_rng(m * 11 + n + k)
+    x_bits = randn_bf16(rng, (m, k))
+    w = rng.integers(-128, 128, (n, k)).astype(np.int8)
+    s_bits = O.f32_to_bf16(rng.uniform(1e-3, 1e-2, n).astype(np.float32))
+    out = torch.full((m, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+    ops.channel_gemv(to_dev(x_bits), to_dev(w), to_dev(s_bits), out)
+    torch.cuda.synchronize()
+    check_gemv(bf16_bits(out), x_bits, w, s_bits)
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 5000, 16384), (5, 600, 12288), (8, 300, 12288),
                                    (16, 70, 9216)])
 def test_long_k_kernels(ops, m, n, k):
