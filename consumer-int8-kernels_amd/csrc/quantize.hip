@@ -11,7 +11,8 @@
 // divides only near half-integers (codes8 in ci8_device.h), with the same codes.
 //
 // Layout: one, two or four waves own a row (four past 1024 values, so a lane holds
-// at most a few 16-byte packs) and keep it in registers between the max reduction and the
+// at most a few 16-byte packs; eight when a few rows of 2,561..4,096 values leave most
+// CUs idle) and keep it in registers between the max reduction and the
 // store, so HBM sees a single read of x and a single write of the codes, with 16-byte
 // loads and 8-byte nontemporal stores fully coalesced across the wave.
 #include "ci8_device.h"
@@ -31,12 +32,13 @@ __device__ __forceinline__ float wave_max(float v) {
 // Vector path. Requires k % 8 == 0, x 16-byte aligned, codes 8-byte aligned.
 // kWaves waves cooperate on one row when kWaves > 1 (very wide rows).
 // Grouped: output row o reads input row (o % m) * groups + o / m ([m,g,k] -> [g,m,k]).
+// Workgroups hold four waves (1, 2 or 4 rows), or kWaves waves and one row for kWaves > 4.
 template <int kPacks, int kWaves, bool kGrouped, bool kNt>
-__global__ void __launch_bounds__(256) quantize_rows_vec_kernel(
+__global__ void __launch_bounds__(kWaves > 4 ? 64 * kWaves : 256) quantize_rows_vec_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ codes, float* __restrict__ scales,
     int rows, int k, int m, int groups) {
-  constexpr int kRowsPerBlock = 4 / kWaves;
-  __shared__ float partial[4];
+  constexpr int kRowsPerBlock = kWaves > 4 ? 1 : 4 / kWaves;
+  __shared__ float partial[kWaves > 4 ? kWaves : 4];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int out_row = blockIdx.x * kRowsPerBlock + wave / kWaves;
@@ -113,12 +115,14 @@ hipError_t dispatch(const void* x, int8_t* codes, float* scales, int rows, int k
   const bool nt = int64_t(rows) * k * 2 > kMallBytes;
 #define CI8_QW(W, P)                                                                       \
   if (packs <= (W) * (P)) {                                                                \
-    const int blocks = (rows + 4 / (W) - 1) / (4 / (W));                                   \
+    constexpr int kPerBlock = (W) > 4 ? 1 : 4 / (W);                                       \
+    constexpr int kThreads = (W) > 4 ? 64 * (W) : 256;                                     \
+    const int blocks = (rows + kPerBlock - 1) / kPerBlock;                                 \
     if (nt)                                                                                \
-      quantize_rows_vec_kernel<P, W, kGrouped, true><<<blocks, 256, 0, stream>>>(           \
+      quantize_rows_vec_kernel<P, W, kGrouped, true><<<blocks, kThreads, 0, stream>>>(      \
           src, codes, scales, rows, k, m, groups);                                         \
     else                                                                                   \
-      quantize_rows_vec_kernel<P, W, kGrouped, false><<<blocks, 256, 0, stream>>>(          \
+      quantize_rows_vec_kernel<P, W, kGrouped, false><<<blocks, kThreads, 0, stream>>>(     \
           src, codes, scales, rows, k, m, groups);                                         \
     return hipGetLastError();                                                              \
   }
@@ -127,6 +131,16 @@ hipError_t dispatch(const void* x, int8_t* codes, float* scales, int rows, int k
   // row): [128, 4096] 3.04 / 4.05 / 7.33, [16, 5120] 3.76 / 5.20 / 8.12, [256, 5120]
   // 3.37 / 4.31 / 7.11, [4096, 5120] 13.87 / 14.42 / 15.84: more waves keep more loads
   // in flight and let a row's stores start sooner.
+  // When the rows do not fill the chip (configs[0]'s 128 rows on 256 CUs) the op is one
+  // memory latency long, and eight waves of one pack per lane shorten it a little
+  // (measured on MI355X in configs[0]'s quantize + fused_channel_mm step, 128 x 4096,
+  // against four waves of two packs, same box and process: 11.80-11.86 against
+  // 12.04-12.18 us on one box, 12.27-12.48 against 12.41-12.57 us on another; identical
+  // codes).
+  const bool few_rows = rows <= 256;
+  if (vec && few_rows && packs > 4 && packs <= 8) {
+    CI8_QW(8, 1)
+  }
   if (vec) {
     CI8_QW(1, 1) CI8_QW(2, 1) CI8_QW(4, 1) CI8_QW(4, 2) CI8_QW(4, 3) CI8_QW(4, 4)
     CI8_QW(4, 5) CI8_QW(4, 6) CI8_QW(4, 7) CI8_QW(4, 8) CI8_QW(4, 9) CI8_QW(4, 10)

@@ -46,7 +46,9 @@ def test_quantize_rows_preserves_zero_rows_and_round_to_even(ops, width, rows, m
 
 SHAPES = [(1, 1), (3, 7), (5, 100), (2, 512), (4, 4096), (17, 5120), (1024, 5120),
           (4096, 5120), (7, 17408), (9, 4100), (33, 20000), (3, 20480), (2, 65536),
-          (2, 70000), (5, 129)]
+          (2, 70000), (5, 129),
+          # eight waves per row (at most 256 rows of 2,561..4,096 values), and either side
+          (128, 4096), (256, 2568), (100, 2576), (257, 3072), (1, 2560)]
 
 
 @pytest.mark.parametrize("rows,width", SHAPES)
