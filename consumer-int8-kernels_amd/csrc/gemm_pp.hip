@@ -50,6 +50,8 @@
 //      2t + 1.
 // In a tile's last stage group 0 copies the next tile's A(0), and in its last two group
 // 1 copies the next tile's W(0) and W(1); those are waited for at the tile switch.
+// Stage t of a tile is K stage (t + t0) % ns with a per-tile start t0, so the tiles of an
+// XCD that share a panel do not fetch its K slices all at once (gemm_pp_kernel.h).
 // A W wave has 7 copies per stage against an A wave's 8; its eighth reads nothing into a
 // junk KiB, which keeps the copy sequence identical and branch-free.
 //

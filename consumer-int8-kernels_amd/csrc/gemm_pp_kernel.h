@@ -123,7 +123,18 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
   const int c_row = lane >> 3;
   const int c_chunk = (lane & 7) ^ c_row;
   uint32_t c_off[C::kCopies];
+  // K order of a tile: tile (mt, nt) (m0 = 256 mt, n0 = 224 nt) copies its K stages in the
+  // order t0, t0 + 1, ..., ns - 1, 0, ..., t0 - 1 with t0 = (mt + nt) % 8 (mod ns). The 32
+  // tiles an XCD runs together are 4 m x 8 n tiles of the raster, so the 4 that share a W
+  // panel and the 8 that share an A panel start at distinct stages and reach each K slice
+  // a stage or more apart instead of together: the first to arrive fetches the slice into
+  // the XCD's L2, the rest find it there. The INT32 sums are exact in any order, so the
+  // output bits are the same. Measured on MI355X at configs[2] (same process, three runs):
+  // 272.0-274.9 against 278.1-285.7 us (starting W sharers only 2 stages apart: 272.1-276.0;
+  // A sharers only: 288.3-290.4; 2 stages apart or 16 offsets: no gain).
+  int c_t0 = 0;
   auto set_copy_tile = [&] __device__(int m0, int n0) __attribute__((always_inline)) {
+    c_t0 = (m0 / C::BM + n0 / C::BN) % 8 % ns;
 #pragma unroll
     for (int i = 0; i < C::kCopies; ++i) {
       const int row = (copies_a ? m0 : n0) + (i * C::WM + sub) * 8 + c_row;
@@ -138,7 +149,7 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
   auto copy = [&] __device__(int dst, int t, int i) __attribute__((always_inline)) {
     int to = dst + i * C::WM * 1024;
     if (i == C::kCopies - 1) to = copies_a ? to : C::kJunk;
-    const int k0 = t * C::BK;
+    const int k0 = (t + c_t0 < ns ? t + c_t0 : t + c_t0 - ns) * C::BK;  // stage t of the tile's order
     uint32_t off = c_off[i];
     if (!kExactK && off != kOutOfRange && k0 + c_chunk * 16 >= k) off = kOutOfRange;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(c_rsrc, reinterpret_cast<lds_void*>(lds + to), 16,

@@ -62,11 +62,12 @@ def test_stamped_kernel_matches_fused_channel_mm(ops, m, n, k, mode):
         assert bool((phases == 0).all())
     else:
         # Every phase sum is non-negative, the compute phase of both waves is nonzero, and
-        # a wave's sums add up to its own start-to-end time less the few cycles between
-        # its last stamp and its end-time read.
+        # a wave's sums add up to its own start-to-end time less the cycles between its
+        # last stamp and its end-time read: two s_memtime round trips, whose return can
+        # queue behind other scalar requests (measured 112-632 cycles per workgroup).
         assert bool((phases >= 0).all())
         assert bool((rec[:, 4 + 3] > 0).all()) and bool((rec[:, 4 + kinds + 3] > 0).all())
         for first, start, end in ((4, 0, 1), (4 + kinds, start4, end4)):
             total = rec[:, first:first + kinds].sum(dim=1)
             span = rec[:, end] - rec[:, start]
-            assert bool((total <= span).all() and (total >= span - 500).all()), (first, total, span)
+            assert bool((total <= span).all() and (total >= span - 1000).all()), (first, total, span)
