@@ -227,24 +227,29 @@ def hbm_stream_probe(torch, cus: int) -> dict:
 
     lib = ctypes.CDLL(str(REPO / "consumer-int8-kernels_amd" / "consumer_int8" / "libci8_probe.so"))
     lib.ci8probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
-                                         ctypes.c_int, ctypes.c_void_p]
+                                         ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     lib.ci8probe_stream_read2_write1.argtypes = [ctypes.c_void_p, ctypes.c_int64,
                                                  ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     out = {}
+    # Random bytes, like the weights the GEMV reads (the time depends on the data).
     read_bytes = GEMV_N * GEMV_K
-    srcs = [torch.ones(read_bytes, dtype=torch.uint8, device="cuda") for _ in range(4)]
+    gen = torch.Generator(device="cuda").manual_seed(20261311)
+    srcs = [torch.randint(0, 256, (read_bytes,), generator=gen, dtype=torch.uint8, device="cuda")
+            for _ in range(4)]
     sink = torch.zeros(4, dtype=torch.int32, device="cuda")
     best = None
-    for blocks in (cus * 4, cus * 8, cus * 16):
-        calls = [lambda s=s, b=blocks: lib.ci8probe_stream_read(
-                     s.data_ptr(), read_bytes, sink.data_ptr(), b,
-                     torch.cuda.current_stream().cuda_stream) for s in srcs]
-        for c in calls:
-            assert c() == 0
-        mean_us, _ = time_kernel(torch, calls, 8)
-        if best is None or mean_us < best[0]:
-            best = (mean_us, blocks)
+    for variant in (0, 1):  # 8 plain / 16 nontemporal loads in flight per thread
+        for blocks in (cus * 4, cus * 8, cus * 16):
+            calls = [lambda s=s, b=blocks, v=variant: lib.ci8probe_stream_read(
+                         s.data_ptr(), read_bytes, sink.data_ptr(), b, v,
+                         torch.cuda.current_stream().cuda_stream) for s in srcs]
+            for c in calls:
+                assert c() == 0
+            mean_us, _ = time_kernel(torch, calls, 8)
+            if best is None or mean_us < best[0]:
+                best = (mean_us, blocks, variant)
     out["read"] = {"bytes": read_bytes, "mean_us": round(best[0], 2), "blocks": best[1],
+                   "variant": ["8 plain loads per thread", "16 nontemporal loads per thread"][best[2]],
                    "gbs": round(read_bytes / (best[0] * 1e-6) / 1e9, 1)}
     del srcs
     rw_read = 2 * M * K

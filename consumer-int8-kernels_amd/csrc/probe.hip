@@ -64,17 +64,20 @@ __global__ void __launch_bounds__(256) mfma_loop_kernel(int rounds, int64_t* rec
 // of a BF16 -> INT8 quantizer, without its per-row dependency). Each thread keeps 8 loads
 // in flight over a grid-stride loop; the loaded words are folded into a value that is
 // stored only if it matches a sentinel, so no load is dead.
+// kIn loads in flight per thread; kNt marks them nontemporal.
+template <int kIn, bool kNt>
 __global__ void __launch_bounds__(256) stream_read_kernel(const i32x4* __restrict__ src,
                                                           int64_t units, int32_t* sink) {
   const int64_t stride = int64_t(gridDim.x) * 256;
   int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   int32_t fold = 0;
-  for (; i + 7 * stride < units; i += 8 * stride) {
-    i32x4 v[8];
+  for (; i + (kIn - 1) * stride < units; i += kIn * stride) {
+    i32x4 v[kIn];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = src[i + j * stride];
+    for (int j = 0; j < kIn; ++j)
+      v[j] = kNt ? __builtin_nontemporal_load(src + i + j * stride) : src[i + j * stride];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) fold ^= v[j][0] ^ v[j][1] ^ v[j][2] ^ v[j][3];
+    for (int j = 0; j < kIn; ++j) fold ^= v[j][0] ^ v[j][1] ^ v[j][2] ^ v[j][3];
   }
   for (; i < units; i += stride) {
     const i32x4 v = src[i];
@@ -109,12 +112,21 @@ __global__ void __launch_bounds__(256) stream_read2_write1_kernel(const i32x4* _
 
 extern "C" {
 
-// Reads `bytes` (a multiple of 16) from `src` with `blocks` workgroups of 256 threads.
-int ci8probe_stream_read(const void* src, int64_t bytes, int32_t* sink, int blocks, void* stream) {
-  if (src == nullptr || sink == nullptr || bytes <= 0 || bytes % 16 || blocks <= 0)
+// Reads `bytes` (a multiple of 16) from `src` with `blocks` workgroups of 256 threads;
+// variant 0: 8 plain loads in flight per thread, 1: 16 nontemporal loads (measured on
+// MI355X over 89 MB of random bytes: 14.7 us at 2,048 workgroups against 15.0 us for
+// variant 0 at its best grid).
+int ci8probe_stream_read(const void* src, int64_t bytes, int32_t* sink, int blocks, int variant,
+                         void* stream) {
+  if (src == nullptr || sink == nullptr || bytes <= 0 || bytes % 16 || blocks <= 0 ||
+      variant < 0 || variant > 1)
     return int(hipErrorInvalidValue);
-  stream_read_kernel<<<blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const i32x4*>(src), bytes / 16, sink);
+  if (variant == 0)
+    stream_read_kernel<8, false><<<blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const i32x4*>(src), bytes / 16, sink);
+  else
+    stream_read_kernel<16, true><<<blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const i32x4*>(src), bytes / 16, sink);
   return int(hipGetLastError());
 }
 

@@ -34,16 +34,20 @@ def test_stream_probes_export_and_reject_bad_arguments():
     """The HBM stream probes bench.py times (plain read; read 2 / write 1) validate their
     arguments before any HIP call."""
     lib = ctypes.CDLL(str(PROBE_PATH))
-    for name in ("ci8probe_stream_read", "ci8probe_stream_read2_write1"):
-        fn = getattr(lib, name)
-        fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
-                       ctypes.c_void_p]
-        buf = ctypes.c_void_p(0x10000)
+    read = lib.ci8probe_stream_read
+    read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                     ctypes.c_void_p]
+    rw = lib.ci8probe_stream_read2_write1
+    rw.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    buf = ctypes.c_void_p(0x10000)
+    for fn in (lambda *a: read(*a[:4], 0, a[4]), lambda *a: read(*a[:4], 1, a[4]), rw):
         assert fn(None, 1024, buf, 256, None) != 0          # no source
         assert fn(buf, 1024, None, 256, None) != 0          # no sink / destination
         assert fn(buf, 1000, buf, 256, None) != 0           # not a multiple of 16 bytes
         assert fn(buf, 0, buf, 256, None) != 0              # empty
         assert fn(buf, 1024, buf, 0, None) != 0             # no workgroups
+    assert read(buf, 1024, buf, 256, 2, None) != 0          # no such variant
+    assert read(buf, 1024, buf, 256, -1, None) != 0
 
 
 def test_stamped_gemm_rejects_bad_arguments_before_any_hip_call():
