@@ -1240,15 +1240,14 @@ bool wide_tiles_pay(int m, int n, int cus) {
   return rounds256 * 256 < rounds224 * 224;
 }
 
-// Whether the persistent 224-wide kernel (one tile per CU per round, about 1.2x the MFMA
-// rate of the 256-wide kernel) finishes sooner than 256-wide tiles: rounds x width,
-// weighted by that rate.
+// Whether the persistent kernel (one tile per CU per round, about 1.2x the MFMA rate of
+// the 256-wide kernel) finishes sooner than 256-wide tiles: the cost of its column plan
+// (pp_plan: rounds x width) against rounds x 256, weighted by that rate.
 bool pp_beats_wide_tiles(int m, int n, int cus) {
   if (cus <= 0) return false;
   const int64_t tiles_m = (m + 255) / 256;
-  const int64_t rounds224 = (tiles_m * ((n + 223) / 224) + cus - 1) / cus;
   const int64_t rounds256 = (tiles_m * ((n + 255) / 256) + cus - 1) / cus;
-  return rounds224 * 224 * 6 <= rounds256 * 256 * 7;
+  return pp_plan(m, n, cus).cost * 6 <= rounds256 * 256 * 7;
 }
 
 // Largest M the small-M kernel (gemm_small.hip) takes under schedule 0.
@@ -1267,8 +1266,8 @@ hipError_t dispatch(const int8_t* a, const void* w, const float* sa, const void*
   // (gemm_pp.hip) for either weight code (its epilogue reads the channel scales 8 bytes
   // at a time) in place of the 224-wide one, and also in place of the 256-wide one
   // unless that needs far fewer rounds: per MFMA it is about 1.2x as fast (configs[3],
-  // M = 16384, K = 17408, N = 5120: 6 rounds of 224-wide tiles beat 5 of 256-wide; M = N
-  // = 4096: 2 rounds lose to 1).
+  // M = 16384, K = 17408, N = 5120: 5 rounds of 224-wide tiles and one of 160-wide beat 5
+  // rounds of 256-wide; M = N = 4096: 2 rounds lose to 1).
   if constexpr (!kWorkspace) {
     if (schedule == 0 && m >= 1024 && n % 4 == 0 && reinterpret_cast<uintptr_t>(sw) % 8 == 0 &&
         (choice == 4 || pp_beats_wide_tiles(m, n, cus)))

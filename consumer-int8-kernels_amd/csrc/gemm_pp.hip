@@ -8,7 +8,11 @@
 // per four bytes after each W fragment read.
 //
 // Persistent: one workgroup of eight waves per CU walks the 256 (m) x 224 (n) output
-// tiles b, b + grid, ... (grid = CU count). The copy stream runs on across tiles: the K
+// tiles b, b + grid, ... (grid = CU count). Where the 224-wide tiles would leave the last
+// round partly empty and 160-wide tiles fill it, the columns are split between two
+// launches (pp_plan below): whole rounds of 224-wide tiles, then 160-wide tiles over the
+// rest (configs[3], M = 16384, N = 5120: 5 rounds over 4480 columns, then one round of
+// 256 x 160 tiles over 640, in place of 5.75 rounds of 224-wide tiles). The copy stream runs on across tiles: the K
 // stages g = r * ns + t of the whole launch (tile r, stage t) use ring slots g % 2 (A)
 // and g % 3 (W), and a tile's last stages copy the next tile's first stages just as they
 // copy their own, so the tile switch issues no copies and the address unit is free for
@@ -66,29 +70,75 @@
 
 namespace ci8 {
 
+// Time of a round of 160-wide tiles, in units where a round of 224-wide tiles takes 224
+// (measured on MI355X at configs[3], M = 16384, K = 17408: 5 rounds of 224-wide tiles
+// over N = 4480 took 966-978 us, and the split launch over N = 5120 1114-1129 us, so the
+// 160-wide round and the second launch took ~0.8 of a 224-wide round).
+//
+// The split gains less than its rounds suggest: the chip runs at its power limit, so a
+// partly filled last round runs faster per tile than a full one. At configs[3] the single
+// launch's sixth round (192 of 256 CUs busy, 672 columns for 640) took ~161 us against
+// ~195 us for a full round, and the split launch measured 1114-1129 against 1131-1145 us
+// (same process, alternating, identical outputs): about 1%, mostly the 32 padded columns
+// that the 160-wide tiles do not compute.
+constexpr int64_t kNarrowRoundCost = 180;
+
+PPPlan pp_plan(int m, int n, int cus) {
+  const int64_t tiles_m = (m + PPConfig::BM - 1) / PPConfig::BM;
+  const int64_t tiles = tiles_m * ((n + PPConfig::BN - 1) / PPConfig::BN);
+  PPPlan plan{0, 0};
+  if (cus <= 0) return plan;
+  plan.cost = (tiles + cus - 1) / cus * PPConfig::BN;
+  // Split: 224-wide tiles over the columns that the launch's whole rounds cover, then
+  // 160-wide tiles over the rest.
+  const int64_t head_tiles_n = tiles / cus * cus / tiles_m;
+  const int64_t n_head = head_tiles_n * PPConfig::BN;
+  if (head_tiles_n == 0 || n_head >= n) return plan;
+  const int64_t head_rounds = (head_tiles_n * tiles_m + cus - 1) / cus;
+  const int64_t tail_tiles =
+      tiles_m * ((n - n_head + PPConfigNarrow::BN - 1) / PPConfigNarrow::BN);
+  const int64_t cost =
+      head_rounds * PPConfig::BN + (tail_tiles + cus - 1) / cus * kNarrowRoundCost;
+  if (cost < plan.cost) plan = PPPlan{int(n_head), cost};
+  return plan;
+}
+
 // Requires a and w 16-byte aligned, sw 8-byte aligned and n % 4 == 0 (the fused op's
 // contract); out needs 2-byte alignment (16-byte aligned rows take 16-byte stores).
 hipError_t launch_pp_gemm(const int8_t* a, const void* w, WeightCode code, const float* sa,
                           const void* sw, void* out, int m, int n, int k, hipStream_t stream) {
-  using C = PPConfig;
-  const int tiles = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
   const int cus = device_cu_count();
-  const int grid = cus > 0 && cus < tiles ? cus : tiles;  // one workgroup per CU
   const bool out16 = (reinterpret_cast<uintptr_t>(out) & 15) == 0;
-  auto launch = [&](auto kernel_constant) {
-    constexpr auto kernel = decltype(kernel_constant)::value;
-    if (const hipError_t e = prepare_lds<kernel>(C::kLdsBytes); e != hipSuccess) return e;
-    kernel<<<grid, C::kThreads, C::kLdsBytes, stream>>>(
-        a, static_cast<const int8_t*>(w), sa, static_cast<const uint16_t*>(sw),
-        static_cast<uint16_t*>(out), m, n, k, out16, nullptr);
-    return hipGetLastError();
+  const bool exact = k % PPConfig::BK == 0;
+  // Columns [c0, c0 + nc) of the output with tiles of width kBN.
+  auto launch = [&](auto width, int c0, int nc) {
+    constexpr int kBN = decltype(width)::value;
+    using C = PPConfigT<kBN>;
+    const int tiles = ((nc + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
+    const int grid = cus > 0 && cus < tiles ? cus : tiles;  // one workgroup per CU
+    const int8_t* wc = static_cast<const int8_t*>(w) + int64_t(c0) * k;
+    const uint16_t* swc = static_cast<const uint16_t*>(sw) + c0;
+    uint16_t* outc = static_cast<uint16_t*>(out) + c0;
+    auto go = [&](auto kernel_constant) {
+      constexpr auto kernel = decltype(kernel_constant)::value;
+      if (const hipError_t e = prepare_lds<kernel>(C::kLdsBytes); e != hipSuccess) return e;
+      kernel<<<grid, C::kThreads, C::kLdsBytes, stream>>>(a, wc, sa, swc, outc, m, nc, k, n,
+                                                           out16, nullptr);
+      return hipGetLastError();
+    };
+    constexpr auto kS = WeightCode::kSigned, kU = WeightCode::kBiasedU8;
+    if (code == kS)
+      return exact ? go(kernel_constant<pp_gemm_kernel<true, kS, 0, kBN>>{})
+                   : go(kernel_constant<pp_gemm_kernel<false, kS, 0, kBN>>{});
+    return exact ? go(kernel_constant<pp_gemm_kernel<true, kU, 0, kBN>>{})
+                 : go(kernel_constant<pp_gemm_kernel<false, kU, 0, kBN>>{});
   };
-  const bool exact = k % C::BK == 0;
-  if (code == WeightCode::kSigned)
-    return exact ? launch(kernel_constant<pp_gemm_kernel<true, WeightCode::kSigned>>{})
-                 : launch(kernel_constant<pp_gemm_kernel<false, WeightCode::kSigned>>{});
-  return exact ? launch(kernel_constant<pp_gemm_kernel<true, WeightCode::kBiasedU8>>{})
-               : launch(kernel_constant<pp_gemm_kernel<false, WeightCode::kBiasedU8>>{});
+  const PPPlan plan = pp_plan(m, n, cus);
+  if (plan.n_head == 0) return launch(std::integral_constant<int, PPConfig::BN>{}, 0, n);
+  if (const hipError_t e = launch(std::integral_constant<int, PPConfig::BN>{}, 0, plan.n_head);
+      e != hipSuccess)
+    return e;
+  return launch(std::integral_constant<int, PPConfigNarrow::BN>{}, plan.n_head, n - plan.n_head);
 }
 
 }  // namespace ci8

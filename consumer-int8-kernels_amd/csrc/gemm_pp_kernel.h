@@ -12,26 +12,38 @@ namespace {
 
 constexpr int kXcds = 8;
 
-struct PPConfig {
-  static constexpr int BM = 256, BN = 224, BK = 128;
+// Tiles of 256 (m) x kBN (n), kBN = 224 (the default) or 160 (the narrow tiles that let
+// a launch end in whole rounds; see launch_pp_gemm). Group g = wave / 4 owns WN = kBN / 2
+// columns of the tile.
+template <int kBN>
+struct PPConfigT {
+  static constexpr int BM = 256, BN = kBN, BK = 128;
   static constexpr int kWaves = 8, kThreads = 512;
   static constexpr int WM = 4;                        // waves along m (per group)
+  static constexpr int WN = BN / 2;                   // columns per group (112 or 80)
   static constexpr int TM = BM / WM / 16;             // 4 m blocks per wave
-  static constexpr int TN = BN / 2 / 16;              // 7 n blocks per wave
+  static constexpr int TN = WN / 16;                  // 7 (or 5) n blocks per wave
   static constexpr int kABlocks = BM * BK / 1024;     // 32 copies of A per stage
-  static constexpr int kWBlocks = BN * BK / 1024;     // 28 copies of W per stage
-  static constexpr int kCopies = kABlocks / WM;       // per wave per stage (8)
+  static constexpr int kWBlocks = BN * BK / 1024;     // 28 (or 20) copies of W per stage
+  static constexpr int kCopies = kABlocks / WM;       // per A wave per stage (8)
+  static constexpr int kWValid = kWBlocks / WM;       // per W wave per stage (7 or 5)
+  // Copies a W wave issues per stage: with 7 the eighth reads nothing into a junk KiB, so
+  // that both groups' copy sequences are alike; with 5 it issues just those.
+  static constexpr int kWCopies = kWValid == kCopies - 1 ? kCopies : kWValid;
+  // Copies go out after fragment reads 0, kCopyEvery, 2 kCopyEvery, ... of the memory
+  // phase's 2 (TM + TN) reads (22 or 18).
+  static constexpr int kCopyEvery = 3 * (kCopies - 1) < 2 * (TM + TN) ? 3 : 2;
   static constexpr int kAStage = BM * BK;             // 32 KB
-  static constexpr int kWStage = BN * BK;             // 28 KB
+  static constexpr int kWStage = BN * BK;             // 28 (or 20) KB
   static constexpr int kWBase = 2 * kAStage;          // A ring: 2 slots, W ring: 3 slots
-  static constexpr int kJunk = kWBase + 3 * kWStage;  // 148 KB
+  static constexpr int kJunk = kWBase + 3 * kWStage;  // 148 (or 124) KB
   static constexpr int kRingBytes = kJunk + 1024;
-  // Epilogue staging (reuses the ring): each wave's 64 x 112 BF16 outputs at a row
-  // stride of 240 bytes (60 dwords: 16 rows written by one ds_write_b64 start in
+  // Epilogue staging (reuses the ring): each wave's 64 x WN BF16 outputs at a row stride
+  // of WN * 2 + 16 bytes (60 or 44 dwords: 16 rows written by one ds_write_b64 start in
   // distinct banks).
-  static constexpr int kEpiRowBytes = (BN / 2) * 2 + 16;
+  static constexpr int kEpiRowBytes = WN * 2 + 16;
   static constexpr int kEpiPassBytes = 16 * kEpiRowBytes;  // one 16-row block per wave
-  // The tile's row scales (256 FP32) and channel scales (224 BF16, copied as 256), copied
+  // The tile's row scales (256 FP32) and channel scales (BN BF16, copied as 256), copied
   // into LDS at the tile start (waves 0-3 their own 64 rows' scales, waves 4 and 5 128
   // channels each, 4 bytes a lane) and read back by the epilogue, so they take no
   // registers through the K loop.
@@ -41,11 +53,15 @@ struct PPConfig {
   // tiles (measured on MI355X against 2, 8 and 16: configs[2] 277-278 against 280-286
   // us at 8; configs[3] 1,108-1,110 against 1,152-1,154 us).
   static constexpr int GROUP_M = 4;
-  static_assert(kCopies * WM == kABlocks && (kCopies - 1) * WM == kWBlocks, "copies");
-  static_assert(3 * (kCopies - 1) < 2 * (TM + TN), "copies fit between the fragment reads");
+  static_assert(kCopies * WM == kABlocks && kWValid * WM == kWBlocks && kWCopies <= kCopies,
+                "copies");
+  static_assert(kCopyEvery * (kCopies - 1) < 2 * (TM + TN), "copies fit between the fragment reads");
+  static_assert(WN % 16 == 0 && BN <= 256, "tile width");
   static_assert(kLdsBytes <= 160 * 1024, "LDS");
   static_assert(kWaves * kEpiPassBytes <= kAStage, "epilogue passes fit in A slot 1");
 };
+using PPConfig = PPConfigT<224>;
+using PPConfigNarrow = PPConfigT<160>;
 
 __device__ __forceinline__ i32x4 lds16(const char __attribute__((address_space(3)))* p) {
   return *reinterpret_cast<const __attribute__((address_space(3))) i32x4*>(p);
@@ -73,12 +89,14 @@ enum PhaseStamp {
 constexpr int kStampWords = 32;
 static_assert(6 + 2 * kStampKinds <= kStampWords, "stamp record");
 
-template <bool kExactK, WeightCode kCode, int kStamps = 0>
-__global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
+// out[row, col] is written at out + row * ldo + col (ldo >= n): a launch may cover a
+// column range of a wider output.
+template <bool kExactK, WeightCode kCode, int kStamps = 0, int kBN = 224>
+__global__ void __launch_bounds__(PPConfigT<kBN>::kThreads, 1) pp_gemm_kernel(
     const int8_t* __restrict__ a, const int8_t* __restrict__ w, const float* __restrict__ sa,
-    const uint16_t* __restrict__ sw, uint16_t* __restrict__ out, int m, int n, int k,
+    const uint16_t* __restrict__ sw, uint16_t* __restrict__ out, int m, int n, int k, int ldo,
     bool out16, int64_t* __restrict__ stamps) {
-  using C = PPConfig;
+  using C = PPConfigT<kBN>;
   extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
   auto* lds = (char __attribute__((address_space(3)))*)(lds_raw);
 
@@ -123,7 +141,7 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
   const int c_row = lane >> 3;
   const int c_chunk = (lane & 7) ^ c_row;
   uint32_t c_off[C::kCopies];
-  // K order of a tile: tile (mt, nt) (m0 = 256 mt, n0 = 224 nt) copies its K stages in the
+  // K order of a tile: tile (mt, nt) (m0 = 256 mt, n0 = BN nt) copies its K stages in the
   // order t0, t0 + 1, ..., ns - 1, 0, ..., t0 - 1 with t0 = (mt + nt) % 8 (mod ns). The 32
   // tiles an XCD runs together are 4 m x 8 n tiles of the raster, so the 4 that share a W
   // panel and the 8 that share an A panel start at distinct stages and reach each K slice
@@ -138,17 +156,17 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
 #pragma unroll
     for (int i = 0; i < C::kCopies; ++i) {
       const int row = (copies_a ? m0 : n0) + (i * C::WM + sub) * 8 + c_row;
-      const bool valid = (copies_a || i < C::kCopies - 1) && row < (copies_a ? m : n);
+      const bool valid = (copies_a || i < C::kWValid) && row < (copies_a ? m : n);
       c_off[i] = valid ? uint32_t(row) * uint32_t(k) + uint32_t(c_chunk * 16) : kOutOfRange;
     }
   };
   // LDS destination of copy i into ring slot `slot`: c_dst0 + slot * c_stride + 4096 i
-  // (integer arithmetic on wave-uniform values), except a W wave's eighth (junk KiB).
+  // (integer arithmetic on wave-uniform values), except a W wave's junk copies.
   const int c_dst0 = (copies_a ? 0 : C::kWBase) + sub * 1024;
   const int c_stride = copies_a ? C::kAStage : C::kWStage;
   auto copy = [&] __device__(int dst, int t, int i) __attribute__((always_inline)) {
     int to = dst + i * C::WM * 1024;
-    if (i == C::kCopies - 1) to = copies_a ? to : C::kJunk;
+    if (i >= C::kWValid) to = copies_a ? to : C::kJunk;
     const int k0 = (t + c_t0 < ns ? t + c_t0 : t + c_t0 - ns) * C::BK;  // stage t of the tile's order
     uint32_t off = c_off[i];
     if (!kExactK && off != kOutOfRange && k0 + c_chunk * 16 >= k) off = kOutOfRange;
@@ -160,10 +178,11 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
   // W(0) and W(1) (group 1) into W slots w_slot0 and w_slot1.
   auto first_copies = [&] __device__(int a_slot, int w_slot0, int w_slot1) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < C::kCopies; ++i) copy(c_dst0 + (copies_a ? a_slot : w_slot0) * c_stride, 0, i);
+    for (int i = 0; i < C::kCopies; ++i)
+      if (copies_a || i < C::kWCopies) copy(c_dst0 + (copies_a ? a_slot : w_slot0) * c_stride, 0, i);
     if (!copies_a && 1 < ns) {
 #pragma unroll
-      for (int i = 0; i < C::kCopies; ++i) copy(c_dst0 + w_slot1 * c_stride, 1, i);
+      for (int i = 0; i < C::kWCopies; ++i) copy(c_dst0 + w_slot1 * c_stride, 1, i);
     }
   };
 
@@ -174,12 +193,13 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
   for (int h = 0; h < 2; ++h) {
     const int swz = (((4 * h + f_group) ^ (f_row & 7)) * 16);
     a_base[h] = (wm * 64 + f_row) * C::BK + swz;
-    w_base[h] = C::kWBase + (group * 112 + f_row) * C::BK + swz;
+    w_base[h] = C::kWBase + (group * C::WN + f_row) * C::BK + swz;
   }
   i32x4 af[2][C::TM], wf[2][C::TN];
-  // Memory phase: the 22 fragments of the stage in A slot a_slot and W slot w_slot, with
-  // (kCopy) this wave's 8 copies of stage copy_t into `dst` after fragment reads 0, 3,
-  // ..., 21. Stages past the end are not copied at all.
+  // Memory phase: the 2 (TM + TN) fragments of the stage in A slot a_slot and W slot
+  // w_slot, with (kCopy) this wave's copies of stage copy_t into `dst` after fragment
+  // reads 0, kCopyEvery, ... (224-wide tiles: 22 reads, 8 copies after reads 0, 3, ...,
+  // 21). Stages past the end are not copied at all.
   auto memory = [&] __device__(int a_slot, int w_slot, int dst, int copy_t, auto with_copies)
                     __attribute__((always_inline)) {
     constexpr bool kCopy = decltype(with_copies)::value;
@@ -193,7 +213,9 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
       else
         wf[h][r - C::TM] = lds16(ws + w_base[h] + (r - C::TM) * 16 * C::BK);
       if constexpr (kCopy)
-        if (q % 3 == 0) copy(dst, copy_t, q / 3);
+        if (q % C::kCopyEvery == 0 && q / C::kCopyEvery < C::kCopies &&
+            (copies_a || q / C::kCopyEvery < C::kWCopies))
+          copy(dst, copy_t, q / C::kCopyEvery);
     }
     __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
     if constexpr (kCode == WeightCode::kBiasedU8) {
@@ -289,7 +311,7 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
         stamp(kStampMemory);
         // Group 1: W(t + 1) landed (W(t + 2), just issued, may be in flight). In the last
         // stage nothing of this tile is left to wait for.
-        if (group == 1 && t + 1 < ns) __builtin_amdgcn_s_waitcnt(vmcnt_imm(C::kCopies));
+        if (group == 1 && t + 1 < ns) __builtin_amdgcn_s_waitcnt(vmcnt_imm(C::kWCopies));
       } else {
         memory(a_slot, w_slot, dst, copy_t, std::false_type{});
         stamp(kStampMemory);
@@ -321,13 +343,13 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
 
-    // Epilogue through LDS, 16 rows of the wave's 64 at a time: the 16 x 112 BF16
-    // results of row block j go to the wave's 3840-byte region of the A slot the tile's
-    // last stage used (the next tile's A(0) is in the other) in the MFMA layout and come
-    // back as 16-byte row chunks, so each store instruction writes whole 224-byte row
-    // pieces (14 lanes per row).
+    // Epilogue through LDS, 16 rows of the wave's 64 at a time: the 16 x WN BF16
+    // results of row block j go to the wave's region of the A slot the tile's last stage
+    // used (the next tile's A(0) is in the other) in the MFMA layout and come back as
+    // 16-byte row chunks, so each store instruction writes whole row pieces of 2 WN
+    // bytes (224-wide tiles: 224 bytes, 14 lanes per row).
     const int row0 = tile_m0 + wm * 64;
-    const int col0 = tile_n0 + group * 112;
+    const int col0 = tile_n0 + group * C::WN;
     auto* region = lds + (a_slot ^ 1) * C::kAStage + wave * C::kEpiPassBytes;
     float rs[C::TM];
     u32x2 s2[C::TN];
@@ -338,9 +360,9 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
 #pragma unroll
     for (int i = 0; i < C::TN; ++i)
       s2[i] = *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>(
-          lds + C::kScaleBase + 4 * C::BM + (group * 112 + i * 16 + f_group * 4) * 2);
-    constexpr int kChunks = 112 / 8;  // 16-byte chunks per output row piece
-    const bool full = out16 && row0 + 64 <= m && col0 + 112 <= n && (n % 8) == 0;
+          lds + C::kScaleBase + 4 * C::BM + (group * C::WN + i * 16 + f_group * 4) * 2);
+    constexpr int kChunks = C::WN / 8;  // 16-byte chunks per output row piece
+    const bool full = out16 && row0 + 64 <= m && col0 + C::WN <= n && (ldo % 8) == 0;
 #pragma unroll
     for (int j = 0; j < C::TM; ++j) {
       auto* rbase = region + f_row * C::kEpiRowBytes + f_group * 8;
@@ -367,7 +389,7 @@ __global__ void __launch_bounds__(PPConfig::kThreads, 1) pp_gemm_kernel(
         const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
             region + row * C::kEpiRowBytes + chunk * 16);
         const int grow = row0 + j * 16 + row, gcol = col0 + chunk * 8;
-        uint16_t* dst = out + int64_t(grow) * n + gcol;
+        uint16_t* dst = out + int64_t(grow) * ldo + gcol;
         if (full) {
           *reinterpret_cast<u32x4*>(dst) = v;
         } else if (grow < m) {

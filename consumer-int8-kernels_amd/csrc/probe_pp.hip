@@ -40,8 +40,8 @@ int ci8probe_pp_gemm_stamped(const int8_t* a, const int8_t* w, const float* sa, 
     constexpr auto kernel = decltype(kernel_constant)::value;
     if (const hipError_t e = ci8::prepare_lds<kernel>(C::kLdsBytes); e != hipSuccess) return e;
     kernel<<<grid, C::kThreads, C::kLdsBytes, static_cast<hipStream_t>(stream)>>>(
-        a, w, sa, static_cast<const uint16_t*>(sw), static_cast<uint16_t*>(out), m, n, k, out16,
-        stamps);
+        a, w, sa, static_cast<const uint16_t*>(sw), static_cast<uint16_t*>(out), m, n, k, n,
+        out16, stamps);
     return hipGetLastError();
   };
   const bool exact = k % C::BK == 0;

@@ -272,6 +272,11 @@ def test_wide_tiles_where_they_fill_the_rounds(ops, biased):
     (2048, 17408, 256, True),    # two stages: group 1 copies the next tile from stage 0
     (2048, 17408, 384, False),   # an odd stage count: ring slots alternate across tiles
     (3000, 9000, 1056, True),    # K tail, ragged M and N tiles
+    # On 256 CUs these split the columns: one whole round of 224-wide tiles, then one of
+    # 160-wide tiles over the rest (a ragged last tile; for N = 15516 rows that are not
+    # 16-byte aligned and ragged M), against two rounds of 224-wide tiles.
+    (1024, 15520, 640, False),
+    (1100, 15516, 1056, True),
 ])
 def test_persistent_tile_switches(ops, m, n, k, biased):
     """Shapes where the persistent kernel runs two or more tiles per workgroup, so each
