@@ -68,10 +68,10 @@ PEAK_BF16_TFLOPS = 2500.0  # dense BF16 MFMA
 GEMV_K, GEMV_N = 5120, 17408
 # HBM-side bytes per GEMM launch at this shape, from two rocprofv3 --pmc runs of this
 # script (FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00; the factors make a plain 512 MiB copy
-# read back its own size): 631.0 MB read + 143.5 MB written. Counters cannot be read
+# read back its own size): 628.4 MB read + 143.5 MB written. Counters cannot be read
 # from inside a timed run, so the value is carried here and re-measured whenever the
 # GEMM kernel changes.
-GEMM_TRAFFIC_BYTES = 774_444_647
+GEMM_TRAFFIC_BYTES = 771_858_240
 
 
 def gemv_bytes(m: int) -> int:
