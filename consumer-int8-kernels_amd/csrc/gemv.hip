@@ -791,7 +791,7 @@ hipError_t run_span(const void* x, const int8_t* w, const void* scale, void* out
 //    waves meet at a barrier once per kBatch blocks (at N = 17408 only at the end),
 //    where 4 threads per (block, batch row) add the 16 waves' partials of one R each
 //    and a quad DPP reduction adds the four R. The order of every sum is fixed.
-template <int kU_, int kG_>
+template <int kU_, int kG_, bool kNt_ = false>
 struct QuadConfig {
   static constexpr int kU = kU_;  // 64-element K units per wave
   static constexpr int kG = kG_;  // batch groups of 4 rows
@@ -800,7 +800,18 @@ struct QuadConfig {
   static constexpr int kN4 = kU / 4, kHas2 = (kU % 4) >= 2, kHas1 = kU % 2;
   static constexpr int kLoads = kN4 + kHas2 + kHas1;  // W loads per block and wave
   static constexpr int kBatch = 32 / kG;              // blocks of partials in LDS
+  // Nontemporal weight loads where every wave's K range and every row are whole 128-byte
+  // lines (K % 2048 == 0, so kU is even and rows start on lines). With kU odd (K = 5120:
+  // 320-byte ranges) neighbouring waves read the two halves of a line, and a nontemporal
+  // first half evicts the line before the second is read. Measured on MI355X (same
+  // process, identical outputs), nontemporal against
+  // plain: K = 8192, N = 8192: m = 2 / 4 / 8 12.9-13.9 / 13.6-13.7 / 15.9-16.3 against
+  // 14.0-14.5 / 14.0-14.4 / 16.6-16.7 us; N = 28672: 35.5-35.7 / 37.4-37.5 / 41.3-43.0
+  // against 39.6 / 39.1-39.4 / 44.0-44.8 us; K = 4096 the same within 0.2 us; K = 5120,
+  // N = 17408: m = 2 / 4 17.1-17.2 / 17.8-18.1 against 15.8 / 16.4-16.5 us.
+  static constexpr bool kNt = kNt_;
   static_assert(kU >= 4 && kU <= 8, "K ranges of 256 to 512 elements");
+  static_assert(!kNt || kU % 2 == 0, "nontemporal loads need whole-line K ranges");
   static_assert(kLoads + 1 <= 63, "vmcnt holds 6 bits");
 };
 
@@ -889,15 +900,16 @@ __global__ void __launch_bounds__(C::kThreads) channel_gemv_quad_kernel(
   u32x4 w4[C::kN4];
   u32x2 w2;
   uint32_t w1;
+  constexpr int kPolicy = C::kNt ? kBufferLoadNontemporal : 0;
   auto issue = [&](int lb, int e) __attribute__((always_inline)) {
     if (e < C::kN4)
       w4[e] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(lb, e), 0, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(lb, e), 0, kPolicy));
     else if (C::kHas2 && e == C::kN4)
       w2 = __builtin_bit_cast(
-          u32x2, __builtin_amdgcn_raw_buffer_load_b64(w_rsrc, w_offset(lb, e), 0, 0));
+          u32x2, __builtin_amdgcn_raw_buffer_load_b64(w_rsrc, w_offset(lb, e), 0, kPolicy));
     else
-      w1 = __builtin_amdgcn_raw_buffer_load_b32(w_rsrc, w_offset(lb, e), 0, 0);
+      w1 = __builtin_amdgcn_raw_buffer_load_b32(w_rsrc, w_offset(lb, e), 0, kPolicy);
   };
 #pragma unroll
   for (int e = 0; e < C::kLoads; ++e) {
@@ -981,7 +993,7 @@ __global__ void __launch_bounds__(C::kThreads) channel_gemv_quad_kernel(
   waitcnt<vmcnt_imm(0)>();  // drain the trailing (out-of-range) loads before exit
 }
 
-template <int kU>
+template <int kU, bool kNt = false>
 hipError_t run_quad(const void* x, const int8_t* w, const void* scale, void* out, int m, int n,
                     int k, int cus, hipStream_t stream) {
   const int grid = min(cus, (n + 3) / 4);
@@ -991,8 +1003,8 @@ hipError_t run_quad(const void* x, const int8_t* w, const void* scale, void* out
                                       static_cast<uint16_t*>(out), m, n, k);
     return hipGetLastError();
   };
-  if (m <= 4) return launch(channel_gemv_quad_kernel<QuadConfig<kU, 1>>);
-  return launch(channel_gemv_quad_kernel<QuadConfig<kU, 2>>);
+  if (m <= 4) return launch(channel_gemv_quad_kernel<QuadConfig<kU, 1, kNt>>);
+  return launch(channel_gemv_quad_kernel<QuadConfig<kU, 2, kNt>>);
 }
 
 }  // namespace
@@ -1009,6 +1021,11 @@ hipError_t launch_channel_gemv(const void* x, const int8_t* w, const void* scale
   // > 8, it loses to the span kernel (one MFMA per 4 batch rows); at m = 1 the row
   // kernel is as fast or faster at N >= 28672.
   if (cus > 0 && k >= 4096 && k <= 8192 && ((m >= 2 && m <= 4) || (m >= 5 && m <= 8 && k > 5120))) {
+    if (k % 2048 == 0) {  // whole-line K ranges and rows: nontemporal weight loads
+      if (k == 4096) return run_quad<4, true>(x, w, scale, out, m, n, k, cus, stream);
+      if (k == 6144) return run_quad<6, true>(x, w, scale, out, m, n, k, cus, stream);
+      return run_quad<8, true>(x, w, scale, out, m, n, k, cus, stream);
+    }
     switch (((k + 63) / 64 + 15) / 16) {
       case 4: return run_quad<4>(x, w, scale, out, m, n, k, cus, stream);
       case 5: return run_quad<5>(x, w, scale, out, m, n, k, cus, stream);
