@@ -307,6 +307,43 @@ def test_persistent_tile_switches(ops, m, n, k, biased):
     full_size_check(a_np, w_signed, sa_np, sw_np, acc, out_bits, samples=8)
 
 
+@pytest.mark.parametrize("biased", [False, True])
+def test_column_split_in_graph_replays(ops, biased):
+    """The column split (a launch of 224-wide tiles over whole rounds, then one of
+    160-wide tiles; M = 1024, N = 15520 on 256 CUs) captured into a HIP graph: three
+    replays, each after eager work that overwrites the output, equal the eager call bit
+    for bit, and the eager call equals the 128 x 128 tiling (schedule 1)."""
+    m, n, k = 1024, 15520, 640
+    rng = np.random.default_rng(15520 + biased)
+    a_np, w_np, sa_np, sw_np = gemm_inputs(rng, m, n, k, biased=biased)
+    w_signed = O.debias(w_np) if biased else w_np
+    a, sa, sw, w, ws_dev = to_dev(a_np), to_dev(sa_np), to_dev(sw_np), to_dev(w_np), to_dev(w_signed)
+    out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    print(f"column split graph replay biased={biased}", flush=True)
+
+    def run():
+        if biased:
+            ops.channel_mm(a, w, sa, sw, out)
+        else:
+            ops.fused_channel_mm(a, w, sa, sw, out, 0)
+
+    run()
+    ref = torch.empty_like(out)
+    ops.fused_channel_mm(a, ws_dev, sa, sw, ref, 1)
+    torch.cuda.synchronize()
+    eager = bf16_bits(out)
+    assert np.array_equal(eager, bf16_bits(ref))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    for rep in range(3):
+        out.fill_(float(rep) - 7.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bf16_bits(out), eager), rep
+
+
 def test_c_abi_fused_matches_oracle(ops, lib):
     from consumer_int8 import _abi
 
