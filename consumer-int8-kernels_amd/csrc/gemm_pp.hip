@@ -12,7 +12,12 @@
 // round partly empty and 160-wide tiles fill it, the columns are split between two
 // launches (pp_plan below): whole rounds of 224-wide tiles, then 160-wide tiles over the
 // rest (configs[3], M = 16384, N = 5120: 5 rounds over 4480 columns, then one round of
-// 256 x 160 tiles over 640, in place of 5.75 rounds of 224-wide tiles). The copy stream runs on across tiles: the K
+// 256 x 160 tiles over 640, in place of 5.75 rounds of 224-wide tiles). The 160-wide
+// kernel is the same source with 5 n blocks per wave, 5 W copies per W wave and a copy
+// after every second fragment read (gemm_pp_kernel.h); the numbers below are the 224-wide
+// kernel's.
+//
+// The copy stream runs on across tiles: the K
 // stages g = r * ns + t of the whole launch (tile r, stage t) use ring slots g % 2 (A)
 // and g % 3 (W), and a tile's last stages copy the next tile's first stages just as they
 // copy their own, so the tile switch issues no copies and the address unit is free for
