@@ -1227,28 +1227,9 @@ using Pipe224 = K128Config<256, 224, 2, 2, 8>;        // 4 waves, 128x112 per wa
 using WLds224 = WLdsConfig<224, 8, true>;             // 4 waves, 64x224 per wave
 using WLds256 = WLdsConfig<256, 8, false>;            // 4 waves, 64x256 per wave
 
-// Whether 256-wide large tiles finish an m x n GEMM sooner than 224-wide ones. A launch
-// runs its tiles in rounds of one per CU, and a round takes time in proportion to the
-// tile width, so the cost of a width is rounds x width. 224 suits N = 17408 at M = 4096
-// (1,248 tiles, 4.9 rounds on 256 CUs, where 256-wide tiles need 4.25 rounds, i.e. 5);
-// 256 suits N = 5120 at M = 16384 (5 full rounds against 5.75).
-bool wide_tiles_pay(int m, int n, int cus) {
-  if (cus <= 0) return false;
-  const int64_t tiles_m = (m + 255) / 256;
-  const int64_t rounds224 = (tiles_m * ((n + 223) / 224) + cus - 1) / cus;
-  const int64_t rounds256 = (tiles_m * ((n + 255) / 256) + cus - 1) / cus;
-  return rounds256 * 256 < rounds224 * 224;
-}
-
-// Whether the persistent kernel (one tile per CU per round, about 1.2x the MFMA rate of
-// the 256-wide kernel) finishes sooner than 256-wide tiles: the cost of its column plan
-// (pp_plan: rounds x width) against rounds x 256, weighted by that rate.
-bool pp_beats_wide_tiles(int m, int n, int cus) {
-  if (cus <= 0) return false;
-  const int64_t tiles_m = (m + 255) / 256;
-  const int64_t rounds256 = (tiles_m * ((n + 255) / 256) + cus - 1) / cus;
-  return pp_plan(m, n, cus).cost * 6 <= rounds256 * 256 * 7;
-}
+// wide_tiles_pay and pp_beats_wide_tiles (tile_plan.h) choose between the 224-wide,
+// 256-wide and persistent kernels.
+static_assert(WLds256::BN == kPlanWideBN && WLds224::BN == kPlanBN, "tile_plan.h widths");
 
 // Largest M the small-M kernel (gemm_small.hip) takes under schedule 0.
 constexpr int kSmallMaxM = 256;

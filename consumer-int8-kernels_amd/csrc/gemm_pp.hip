@@ -75,38 +75,10 @@
 
 namespace ci8 {
 
-// Time of a round of 160-wide tiles, in units where a round of 224-wide tiles takes 224
-// (measured on MI355X at configs[3], M = 16384, K = 17408: 5 rounds of 224-wide tiles
-// over N = 4480 took 966-978 us, and the split launch over N = 5120 1114-1129 us, so the
-// 160-wide round and the second launch took ~0.8 of a 224-wide round).
-//
-// The split gains less than its rounds suggest: the chip runs at its power limit, so a
-// partly filled last round runs faster per tile than a full one. At configs[3] the single
-// launch's sixth round (192 of 256 CUs busy, 672 columns for 640) took ~161 us against
-// ~195 us for a full round, and the split launch measured 1114-1129 against 1131-1145 us
-// (same process, alternating, identical outputs): about 1%, mostly the 32 padded columns
-// that the 160-wide tiles do not compute.
-constexpr int64_t kNarrowRoundCost = 180;
-
-PPPlan pp_plan(int m, int n, int cus) {
-  const int64_t tiles_m = (m + PPConfig::BM - 1) / PPConfig::BM;
-  const int64_t tiles = tiles_m * ((n + PPConfig::BN - 1) / PPConfig::BN);
-  PPPlan plan{0, 0};
-  if (cus <= 0) return plan;
-  plan.cost = (tiles + cus - 1) / cus * PPConfig::BN;
-  // Split: 224-wide tiles over the columns that the launch's whole rounds cover, then
-  // 160-wide tiles over the rest.
-  const int64_t head_tiles_n = tiles / cus * cus / tiles_m;
-  const int64_t n_head = head_tiles_n * PPConfig::BN;
-  if (head_tiles_n == 0 || n_head >= n) return plan;
-  const int64_t head_rounds = (head_tiles_n * tiles_m + cus - 1) / cus;
-  const int64_t tail_tiles =
-      tiles_m * ((n - n_head + PPConfigNarrow::BN - 1) / PPConfigNarrow::BN);
-  const int64_t cost =
-      head_rounds * PPConfig::BN + (tail_tiles + cus - 1) / cus * kNarrowRoundCost;
-  if (cost < plan.cost) plan = PPPlan{int(n_head), cost};
-  return plan;
-}
+// The host plan (tile_plan.h) prices these tiles.
+static_assert(PPConfig::BM == kPlanBM && PPConfig::BN == kPlanBN &&
+                  PPConfigNarrow::BM == kPlanBM && PPConfigNarrow::BN == kPlanNarrowBN,
+              "tile_plan.h prices the kernel's tiles");
 
 // Requires a and w 16-byte aligned, sw 8-byte aligned and n % 4 == 0 (the fused op's
 // contract); out needs 2-byte alignment (16-byte aligned rows take 16-byte stores).

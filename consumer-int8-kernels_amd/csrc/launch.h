@@ -4,6 +4,8 @@
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
 
+#include "tile_plan.h"
+
 namespace ci8 {
 
 hipError_t launch_quantize_rows(const void* x, int8_t* codes, float* scales, int m, int k,
@@ -40,16 +42,6 @@ hipError_t launch_channel_gemm_bytes(const int8_t* a, const void* w, WeightCode 
 hipError_t launch_small_m_gemm(const int8_t* a, const void* w, WeightCode code, const float* sa,
                                const void* sw, void* out, int32_t* workspace, int m, int n,
                                int k, int cus, hipStream_t stream);
-
-// Column plan of the two-waves-per-SIMD GEMM (gemm_pp.hip) at m x n on `cus` CUs: 224-wide
-// tiles over the first n_head columns and 160-wide tiles over the rest (n_head = 0: one
-// launch of 224-wide tiles over all n). `cost` is the planned rounds' time in units where a
-// round of 224-wide tiles takes 224.
-struct PPPlan {
-  int n_head;
-  int64_t cost;
-};
-PPPlan pp_plan(int m, int n, int cus);
 
 // Large-M GEMM with two waves per SIMD (gemm_pp.hip), signed or biased UINT8 weights;
 // identical bits. Requires a and w 16-byte aligned, sw 8-byte aligned, n % 4 == 0.
