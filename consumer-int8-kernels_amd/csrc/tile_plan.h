@@ -19,8 +19,9 @@ constexpr int kPlanBM = 256, kPlanBN = 224, kPlanNarrowBN = 160, kPlanWideBN = 2
 // partly filled last round runs faster per tile than a full one. At configs[3] the single
 // launch's sixth round (192 of 256 CUs busy, 672 columns for 640) took ~161 us against
 // ~195 us for a full round, and the split launch measured 1114-1129 against 1131-1145 us
-// (same process, alternating, identical outputs): about 1%, mostly the 32 padded columns
-// that the 160-wide tiles do not compute.
+// (same process, alternating, identical outputs; at K = 5120, 326.5-327.7 against
+// 328.4-329.8 us): about 1%, mostly the 32 padded columns that the 160-wide tiles do not
+// compute.
 constexpr int64_t kNarrowRoundCost = 180;
 
 // Column plan of the two-waves-per-SIMD GEMM (gemm_pp.hip) at m x n on `cus` CUs: 224-wide
@@ -38,6 +39,12 @@ inline PPPlan pp_plan(int m, int n, int cus) {
   PPPlan plan{0, 0};
   if (cus <= 0) return plan;
   plan.cost = (tiles + cus - 1) / cus * kPlanBN;
+  // A last round that keeps under half the CUs busy runs faster per tile than the split's
+  // round of 160-wide tiles (same process, identical outputs: M = 2048, N = 17408, whose
+  // third round holds 112 tiles, 155.4-155.7 us in one launch against 156.7-157.4 us
+  // split; M = 1100, N = 15516, 94 tiles, 106.4-106.9 us either way).
+  const int64_t last = tiles % cus;
+  if (last == 0 || 2 * last < cus) return plan;
   // Split: 224-wide tiles over the columns that the launch's whole rounds cover, then
   // 160-wide tiles over the rest.
   const int64_t head_tiles_n = tiles / cus * cus / tiles_m;

@@ -272,12 +272,13 @@ def test_wide_tiles_where_they_fill_the_rounds(ops, biased):
     (2048, 17408, 256, True),    # two stages: group 1 copies the next tile from stage 0
     (2048, 17408, 384, False),   # an odd stage count: ring slots alternate across tiles
     (3000, 9000, 1056, True),    # K tail, ragged M and N tiles
-    # On 256 CUs the persistent kernel splits the columns of these (and of the N = 17408
-    # shapes above): whole rounds of 224-wide tiles, then one round of 160-wide tiles over
-    # the rest, here with a ragged last tile, rows that are not 16-byte aligned (N =
-    # 15516) and ragged M (tests/test_tile_plan.py checks the plans).
-    (1100, 15516, 640, False),
-    (1100, 15516, 1056, True),
+    # On 256 CUs the persistent kernel splits the columns of these: a round of 224-wide
+    # tiles, then one of 160-wide tiles over the rest (tests/test_tile_plan.py checks the
+    # plans), with one K stage, a K tail, a ragged last tile, rows that are not 16-byte
+    # aligned (N = 18500) and ragged M.
+    (1024, 23040, 128, True),
+    (1024, 23040, 640, False),
+    (1100, 18500, 1056, True),
 ])
 def test_persistent_tile_switches(ops, m, n, k, biased):
     """Shapes where the persistent kernel runs two or more tiles per workgroup, so each
@@ -311,12 +312,12 @@ def test_persistent_tile_switches(ops, m, n, k, biased):
 @pytest.mark.parametrize("biased", [False, True])
 def test_column_split_in_graph_replays(ops, biased):
     """The column split (a launch of 224-wide tiles over whole rounds, then one of
-    160-wide tiles; M = 2048, N = 17408 on 256 CUs: 2 rounds over 14,336 columns, then
-    160 narrow tiles) captured into a HIP graph: three replays, each after eager work that
+    160-wide tiles; M = 1024, N = 23040 on 256 CUs: a round over 14,336 columns, then
+    220 narrow tiles) captured into a HIP graph: three replays, each after eager work that
     overwrites the output, equal the eager call bit for bit, and the eager call equals the
     128 x 128 tiling (schedule 1)."""
-    m, n, k = 2048, 17408, 640
-    rng = np.random.default_rng(17408 + biased)
+    m, n, k = 1024, 23040, 640
+    rng = np.random.default_rng(23040 + biased)
     a_np, w_np, sa_np, sw_np = gemm_inputs(rng, m, n, k, biased=biased)
     w_signed = O.debias(w_np) if biased else w_np
     a, sa, sw, w, ws_dev = to_dev(a_np), to_dev(sa_np), to_dev(sw_np), to_dev(w_np), to_dev(w_signed)

@@ -20,7 +20,8 @@ using namespace ci8;
 int main() {
   const int cases[][3] = {{4096, 17408, 256}, {16384, 5120, 256}, {4096, 4096, 256},
                           {1024, 15520, 256}, {1100, 15516, 256}, {2048, 17408, 256},
-                          {16384, 5120, 0}, {1024, 128, 256}};
+                          {16384, 5120, 0}, {1024, 128, 256}, {1024, 23040, 256},
+                          {1100, 18500, 256}, {8192, 17408, 256}};
   for (const auto& c : cases) {
     const PPPlan p = pp_plan(c[0], c[1], c[2]);
     std::printf("%d %d %d %d %lld %d %d\n", c[0], c[1], c[2], p.n_head, (long long)p.cost,
@@ -46,30 +47,39 @@ def test_tile_plans(tmp_path):
         if line:
             m, n, cus, n_head, cost, wide, pp = map(int, line.split())
             got[(m, n, cus)] = (n_head, cost, wide, pp)
-    # 16 x 78 = 1,248 tiles, 4.875 rounds -> 5 x 224; whole rounds would cover
-    # 64 column tiles (14,336 columns) and leave 3,072 for 20 x 16 = 320 narrow tiles, two
-    # rounds: 4 x 224 + 2 x 180 = 1,256 > 1,120, so one launch. 256-wide: 16 x 68 = 1,088
-    # tiles, 5 rounds (1,280): the persistent kernel wins (1,120 x 6 <= 1,280 x 7).
+    # 16 x 78 = 1,248 tiles, 4.875 rounds -> 5 x 224; the last round holds 224
+    # tiles, but whole rounds would cover 64 column tiles (14,336 columns) and leave 3,072
+    # for 20 x 16 = 320 narrow tiles, two rounds: 4 x 224 + 2 x 180 = 1,256 > 1,120, so
+    # one launch. 256-wide: 16 x 68 = 1,088 tiles, 5 rounds (1,280): the persistent kernel
+    # wins (1,120 x 6 <= 1,280 x 7).
     assert got[(4096, 17408, 256)] == (0, 1120, 0, 1)
-    # 64 x 23 = 1,472 tiles, 5.75 rounds -> 6 x 224 = 1,344; split after 5
-    # rounds = 1,280 tiles = 20 column tiles (4,480 columns), tail 640 = 4 x 160, 256
-    # tiles, one round: 5 x 224 + 180 = 1,300.
+    # 64 x 23 = 1,472 tiles, 5.75 rounds -> 6 x 224 = 1,344, last round 192
+    # tiles; split after 5 rounds = 1,280 tiles = 20 column tiles (4,480 columns), tail 640
+    # = 4 x 160, 256 tiles, one round: 5 x 224 + 180 = 1,300.
     assert got[(16384, 5120, 256)] == (4480, 1300, 1, 1)
-    # M = N = 4096: 304 tiles, 2 rounds; a split (3,584 + 512 columns, 224 + 180 = 404)
-    # still loses to one round of 256-wide tiles (404 x 6 > 256 x 7).
-    assert got[(4096, 4096, 256)] == (3584, 404, 1, 0)
-    # 4 x 70 = 280 tiles (2 rounds, 448) against one round of 224-wide tiles over 64 column
-    # tiles plus 8 (7.4) narrow column tiles x 4 (404); but 4 x 61 = 244 tiles of 256-wide
-    # fill one round (256), so the 256-wide kernel takes it.
-    assert got[(1024, 15520, 256)] == (14336, 404, 1, 0)
-    # 5 x 70 = 350 tiles; 256 // 5 = 51 column tiles (11,424 columns) in one round, the
-    # other 4,092 columns as 5 x 26 = 130 narrow tiles; 256-wide tiles need 5 x 61 = 305,
-    # two rounds (512), so the persistent kernel runs it, split.
-    assert got[(1100, 15516, 256)] == (11424, 404, 0, 1)
-    # 8 x 78 = 624 tiles, 2.44 rounds -> 672; split after 2 rounds: 64 column tiles, tail
-    # 3,072 columns = 20 narrow column tiles x 8 = 160 tiles: 448 + 180 = 628.
-    assert got[(2048, 17408, 256)] == (14336, 628, 0, 1)
+    # M = N = 4096: 304 tiles, 2 rounds (448), the second 48 tiles: no split; one round of
+    # 256-wide tiles (16 x 16) wins (448 x 6 > 256 x 7).
+    assert got[(4096, 4096, 256)] == (0, 448, 1, 0)
+    # 4 x 70 = 280 tiles, the second round 24: no split; 4 x 61 = 244 tiles of 256-wide
+    # fill one round, so the 256-wide kernel takes it.
+    assert got[(1024, 15520, 256)] == (0, 448, 1, 0)
+    # 5 x 70 = 350 tiles, the second round 94 (under half): one launch of 224-wide tiles
+    # (256-wide: 5 x 61 = 305 tiles, also 2 rounds, 512).
+    assert got[(1100, 15516, 256)] == (0, 448, 0, 1)
+    # 8 x 78 = 624 tiles, the third round 112 tiles (under half): one launch, 3 x 224.
+    assert got[(2048, 17408, 256)] == (0, 672, 0, 1)
     # No CU count: no plan, no preference.
     assert got[(16384, 5120, 0)] == (0, 0, 0, 0)
     # Fewer tiles than CUs: one round, nothing to split.
     assert got[(1024, 128, 256)] == (0, 224, 0, 1)
+    # The GPU tests' split shapes. 4 x 103 = 412 tiles, the second round 156: one round of
+    # 224-wide tiles over 64 column tiles (14,336 columns), then 8,704 columns as 55 x 4 =
+    # 220 narrow tiles: 224 + 180 = 404 < 448 (256-wide: 4 x 90 = 360 tiles, 2 rounds).
+    assert got[(1024, 23040, 256)] == (14336, 404, 0, 1)
+    # 5 x 83 = 415 tiles, the second round 159; 256 // 5 = 51 column tiles (11,424
+    # columns), then 7,076 columns as 45 x 5 = 225 narrow tiles.
+    assert got[(1100, 18500, 256)] == (11424, 404, 0, 1)
+    # 32 x 78 = 2,496 tiles, 9.75 rounds (2,240), last round 192: 9 rounds = 2,304 tiles =
+    # 72 column tiles (16,128 columns), 1,280 columns = 8 x 32 = 256 narrow tiles:
+    # 9 x 224 + 180 = 2,196.
+    assert got[(8192, 17408, 256)] == (16128, 2196, 0, 1)
