@@ -190,7 +190,14 @@ struct GgufSpanConfig {
   static constexpr int kSpb = kSpb_;  // 64-element K blocks per range
   static constexpr int kBatch = 8;    // blocks per partial-sum reduction (128 KiB of LDS)
   static constexpr int kThreads = 64 * kS;
-  static_assert(2 * kSpb - 2 <= 63, "vmcnt holds 6 bits");
+  // A wave's block scales: with kSpb <= 5 the row's 2 kSpb scales of its K range come in
+  // one or two loads per block (one b64 / b128, or b128 + b32); at kSpb = 8 the second
+  // copy of them would not fit the 128 registers a lane has at 16 waves per CU, so each
+  // slot loads its own 2-byte scale.
+  static constexpr bool kBlockScales = kSpb <= 5;
+  static constexpr int kSLoads = kSpb == 2 || kSpb == 4 ? 1 : 2;
+  static_assert(kSpb == 2 || kSpb == 4 || kSpb == 5 || kSpb == 8, "scale load shapes");
+  static_assert(2 * kSpb - 2 <= 63 && kSpb - 1 + kSLoads <= 63, "vmcnt holds 6 bits");
 };
 
 template <int kImm>
@@ -248,11 +255,18 @@ __global__ void __launch_bounds__(C::kThreads) gguf_q8_span_kernel(
                ? uint32_t(channel) * uint32_t(k) + uint32_t((kb_first + s) * 64 + q * 16)
                : kOutOfRange;
   };
-  auto s_offset = [&](int lb, int s) __attribute__((always_inline)) {
+  // Slot s's scale (2 bytes) in block lb.
+  auto s_slot_offset = [&](int lb, int s) __attribute__((always_inline)) {
     const int channel = c0 + lb * 16 + row;
     return slot_valid(lb, s)
                ? (uint32_t(channel) * uint32_t(k / 32) + uint32_t((kb_first + s) * 2 + q / 2)) * 2u
                : kOutOfRange;
+  };
+  // First of the row's block scales of this wave's K range, in block lb.
+  auto s_offset = [&](int lb) __attribute__((always_inline)) {
+    const int channel = c0 + lb * 16 + row;
+    return slot_valid(lb, 0) ? (uint32_t(channel) * uint32_t(k / 32) + uint32_t(kb_first * 2)) * 2u
+                             : kOutOfRange;
   };
 
   // Adds the partials of local blocks [lb0, lb0 + count) in range order and stores them.
@@ -295,21 +309,61 @@ __global__ void __launch_bounds__(C::kThreads) gguf_q8_span_kernel(
                                                          0, 0));
     }
     u32x4 wv[C::kSpb];
-    uint32_t sv[C::kSpb];
+    // kBlockScales: the row's 2 kSpb block scales of this wave's K range are kSpb dwords
+    // (dword-aligned: K % 64 == 0), loaded once per block in C::kSLoads loads; slot s of
+    // lane group q uses half (q / 2) of dword s.
+    uint32_t sn[C::kSpb];
+    auto load_scales = [&](int lb) __attribute__((always_inline)) {
+      if constexpr (C::kBlockScales) {
+        const uint32_t off = s_offset(lb);
+        if constexpr (C::kSpb == 2) {
+          const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(s_rsrc, off, 0, 0));
+          sn[0] = v[0];
+          sn[1] = v[1];
+        } else {
+          const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(s_rsrc, off, 0, 0));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sn[e] = v[e];
+          if constexpr (C::kSpb == 5)
+            sn[4] = __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, off == kOutOfRange ? off : off + 16u, 0, 0);
+        }
+      }
+    };
+    load_scales(0);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < C::kSpb; ++s) {
       wv[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(0, s), 0, 0));
-      sv[s] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, s_offset(0, s), 0, 0);
+      if constexpr (!C::kBlockScales) sn[s] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, s_slot_offset(0, s), 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
 
     for (int lb = 0; lb < nlocal; ++lb) {
       f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+      uint32_t sd[C::kBlockScales ? C::kSpb : 1];
+      if constexpr (C::kBlockScales) {
+        // S(lb) has landed (the W loads of block lb, issued after it, may be in flight);
+        // the next block's scales go out now.
+        waitcnt<vmcnt_imm(C::kSpb)>();
+#pragma unroll
+        for (int s = 0; s < C::kSpb; ++s) sd[s] = sn[s];
+        __builtin_amdgcn_sched_barrier(0);
+        load_scales(lb + 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
       for (int s = 0; s < C::kSpb; ++s) {
-        waitcnt<vmcnt_imm(2 * C::kSpb - 2)>();  // W(lb, s) and its scale have landed
+        float sc;
+        if constexpr (C::kBlockScales) {
+          // W(lb, s) has landed: after it went out the rest of block lb's W, the next
+          // block's scales and the first s W loads of block lb + 1.
+          waitcnt<vmcnt_imm(C::kSpb - 1 + C::kSLoads)>();
+          sc = f16_to_f32((sd[s] >> (16 * (q >> 1))) & 0xFFFFu);
+        } else {
+          waitcnt<vmcnt_imm(2 * C::kSpb - 2)>();  // W(lb, s) and its scale have landed
+          sc = f16_to_f32(sn[s]);
+        }
         if (s < my_slots) {
-          const float sc = f16_to_f32(sv[s]);
           const u32x4 wq = wv[s];
           const u32x2 d0 = dequant4(wq[0], sc), d1 = dequant4(wq[1], sc);
           const u32x2 d2 = dequant4(wq[2], sc), d3 = dequant4(wq[3], sc);
@@ -318,7 +372,8 @@ __global__ void __launch_bounds__(C::kThreads) gguf_q8_span_kernel(
         }
         wv[s] = __builtin_bit_cast(
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(lb + 1, s), 0, 0));
-        sv[s] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, s_offset(lb + 1, s), 0, 0);
+        if constexpr (!C::kBlockScales)
+          sn[s] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, s_slot_offset(lb + 1, s), 0, 0);
         __builtin_amdgcn_sched_barrier(0);
       }
       if (nchunks == 1) {
