@@ -191,13 +191,13 @@ struct GgufSpanConfig {
   static constexpr int kBatch = 8;    // blocks per partial-sum reduction (128 KiB of LDS)
   static constexpr int kThreads = 64 * kS;
   // A wave's block scales: with kSpb <= 5 the row's 2 kSpb scales of its K range come in
-  // one or two loads per block (one b64 / b128, or b128 + b32); at kSpb = 8 the second
-  // copy of them would not fit the 128 registers a lane has at 16 waves per CU, so each
-  // slot loads its own 2-byte scale.
+  // one or two loads per block (one b64 / b128, or b128 + b32); at kSpb = 8 a second copy
+  // of all 16 would not fit the 128 registers a lane has at 16 waves per CU, so they come
+  // as two 16-byte halves.
   static constexpr bool kBlockScales = kSpb <= 5;
   static constexpr int kSLoads = kSpb == 2 || kSpb == 4 ? 1 : 2;
   static_assert(kSpb == 2 || kSpb == 4 || kSpb == 5 || kSpb == 8, "scale load shapes");
-  static_assert(2 * kSpb - 2 <= 63 && kSpb - 1 + kSLoads <= 63, "vmcnt holds 6 bits");
+  static_assert(kSpb - 1 + kSLoads <= 63, "vmcnt holds 6 bits");
 };
 
 template <int kImm>
@@ -255,13 +255,6 @@ __global__ void __launch_bounds__(C::kThreads) gguf_q8_span_kernel(
                ? uint32_t(channel) * uint32_t(k) + uint32_t((kb_first + s) * 64 + q * 16)
                : kOutOfRange;
   };
-  // Slot s's scale (2 bytes) in block lb.
-  auto s_slot_offset = [&](int lb, int s) __attribute__((always_inline)) {
-    const int channel = c0 + lb * 16 + row;
-    return slot_valid(lb, s)
-               ? (uint32_t(channel) * uint32_t(k / 32) + uint32_t((kb_first + s) * 2 + q / 2)) * 2u
-               : kOutOfRange;
-  };
   // First of the row's block scales of this wave's K range, in block lb.
   auto s_offset = [&](int lb) __attribute__((always_inline)) {
     const int channel = c0 + lb * 16 + row;
@@ -309,60 +302,80 @@ __global__ void __launch_bounds__(C::kThreads) gguf_q8_span_kernel(
                                                          0, 0));
     }
     u32x4 wv[C::kSpb];
-    // kBlockScales: the row's 2 kSpb block scales of this wave's K range are kSpb dwords
-    // (dword-aligned: K % 64 == 0), loaded once per block in C::kSLoads loads; slot s of
-    // lane group q uses half (q / 2) of dword s.
-    uint32_t sn[C::kSpb];
-    auto load_scales = [&](int lb) __attribute__((always_inline)) {
-      if constexpr (C::kBlockScales) {
-        const uint32_t off = s_offset(lb);
-        if constexpr (C::kSpb == 2) {
-          const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(s_rsrc, off, 0, 0));
-          sn[0] = v[0];
-          sn[1] = v[1];
-        } else {
-          const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(s_rsrc, off, 0, 0));
+    // The row's 2 kSpb block scales of this wave's K range are kSpb dwords (dword-aligned:
+    // K % 64 == 0); slot s of lane group q uses half (q / 2) of dword s. With kSpb <= 5
+    // (kBlockScales) they come in C::kSLoads loads per block; with kSpb = 8, as two
+    // 16-byte halves (slots 0-3, 4-7), each loaded half a block before its slots, so a
+    // lane holds 8 scale registers, as it would with a 2-byte load per slot.
+    constexpr int kHeld = C::kBlockScales ? C::kSpb : 4;
+    uint32_t sn[kHeld], sd[kHeld];
+    auto load_scales = [&](int lb, int half) __attribute__((always_inline)) {
+      const uint32_t off = s_offset(lb);
+      if constexpr (C::kSpb == 2) {
+        const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(s_rsrc, off, 0, 0));
+        sn[0] = v[0];
+        sn[1] = v[1];
+      } else {
+        const u32x4 v = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       s_rsrc, off == kOutOfRange ? off : off + 16u * half, 0, 0));
 #pragma unroll
-          for (int e = 0; e < 4; ++e) sn[e] = v[e];
-          if constexpr (C::kSpb == 5)
-            sn[4] = __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, off == kOutOfRange ? off : off + 16u, 0, 0);
-        }
+        for (int e = 0; e < 4; ++e) sn[e] = v[e];
+        if constexpr (C::kSpb == 5)
+          sn[4] = __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, off == kOutOfRange ? off : off + 16u, 0, 0);
       }
     };
-    load_scales(0);
-    __builtin_amdgcn_sched_barrier(0);
+    auto take_scales = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int s = 0; s < C::kSpb; ++s) {
-      wv[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(0, s), 0, 0));
-      if constexpr (!C::kBlockScales) sn[s] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, s_slot_offset(0, s), 0, 0);
+      for (int e = 0; e < kHeld; ++e) sd[e] = sn[e];
       __builtin_amdgcn_sched_barrier(0);
+    };
+    auto load_w = [&](int lb, int s) __attribute__((always_inline)) {
+      wv[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(lb, s), 0, 0));
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    // Prologue, in the order the loop's waits count on: kBlockScales: S(0), W(0, 0..);
+    // halves: W(0, 0..3), S(0, half 0), W(0, 4..7).
+    if constexpr (C::kBlockScales) {
+      load_scales(0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 0; s < C::kSpb; ++s) load_w(0, s);
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) load_w(0, s);
+      load_scales(0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 4; s < 8; ++s) load_w(0, s);
     }
 
     for (int lb = 0; lb < nlocal; ++lb) {
       f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-      uint32_t sd[C::kBlockScales ? C::kSpb : 1];
-      if constexpr (C::kBlockScales) {
-        // S(lb) has landed (the W loads of block lb, issued after it, may be in flight);
-        // the next block's scales go out now.
-        waitcnt<vmcnt_imm(C::kSpb)>();
-#pragma unroll
-        for (int s = 0; s < C::kSpb; ++s) sd[s] = sn[s];
-        __builtin_amdgcn_sched_barrier(0);
-        load_scales(lb + 1);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      // Block lb's scales (kBlockScales) or its first half have landed: the W loads issued
+      // after them (all of block lb's, or its slots 4-7) may be in flight. Their successor
+      // goes out now.
+      waitcnt<vmcnt_imm(C::kBlockScales ? C::kSpb : 4)>();
+      take_scales();
+      load_scales(C::kBlockScales ? lb + 1 : lb, C::kBlockScales ? 0 : 1);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int s = 0; s < C::kSpb; ++s) {
-        float sc;
-        if constexpr (C::kBlockScales) {
-          // W(lb, s) has landed: after it went out the rest of block lb's W, the next
-          // block's scales and the first s W loads of block lb + 1.
-          waitcnt<vmcnt_imm(C::kSpb - 1 + C::kSLoads)>();
-          sc = f16_to_f32((sd[s] >> (16 * (q >> 1))) & 0xFFFFu);
-        } else {
-          waitcnt<vmcnt_imm(2 * C::kSpb - 2)>();  // W(lb, s) and its scale have landed
-          sc = f16_to_f32(sn[s]);
+        if constexpr (!C::kBlockScales) {
+          if (s == 4) {
+            // The second half (issued at slot 0, before the first four W loads of block
+            // lb + 1) has landed; the next block's first half goes out.
+            waitcnt<vmcnt_imm(4)>();
+            take_scales();
+            load_scales(lb + 1, 0);
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
+        // W(lb, s) has landed. Loads after it: kBlockScales: the rest of block lb's W, the
+        // next scales and the first s W loads of block lb + 1 (kSpb - 1 + kSLoads);
+        // halves: the rest of the block's W, two scale halves and W(lb + 1, < s) (9).
+        waitcnt<vmcnt_imm(C::kBlockScales ? C::kSpb - 1 + C::kSLoads : 9)>();
+        const float sc = f16_to_f32((sd[s % kHeld] >> (16 * (q >> 1))) & 0xFFFFu);
         if (s < my_slots) {
           const u32x4 wq = wv[s];
           const u32x2 d0 = dequant4(wq[0], sc), d1 = dequant4(wq[1], sc);
@@ -370,11 +383,7 @@ __global__ void __launch_bounds__(C::kThreads) gguf_q8_span_kernel(
           acc = mfma_bf16(u32x4{d0[0], d0[1], d1[0], d1[1]}, xf[s][0], acc);
           acc = mfma_bf16(u32x4{d2[0], d2[1], d3[0], d3[1]}, xf[s][1], acc);
         }
-        wv[s] = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_offset(lb + 1, s), 0, 0));
-        if constexpr (!C::kBlockScales)
-          sn[s] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, s_slot_offset(lb + 1, s), 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
+        load_w(lb + 1, s);
       }
       if (nchunks == 1) {
         partial[lb % C::kBatch][range][lane] = acc;
