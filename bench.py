@@ -42,6 +42,10 @@ untimed launches of their own before they are timed.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-extras]
                       [--copy-calibration] [--condition-seconds S]
        python bench.py --phase-profile   (the GEMM's per-phase cycle table; no bench line)
+       python bench.py --linear-sweep OUT.json [--fused-only [--fused-paired]
+                      [--fused-schedules S ...]] [--fused-schedule S] [--prefill-only]
+                      [--linear-rows M ...] [--linear-shape N K ...]
+                      (the reference microbenchmark's linear-layer table; no bench line)
 """
 
 from __future__ import annotations
@@ -96,6 +100,18 @@ def parse_args():
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a plain 512 MiB device copy three times (a kernel of known "
                         "traffic that scales FETCH_SIZE / WRITE_SIZE counters)")
+    # The reference microbenchmark's linear-layer options (benchmarks/microbench.py:56-73).
+    p.add_argument("--linear-sweep", metavar="OUTPUT",
+                   help="run the linear-layer sweep (linear_sweep) instead of the bench line, "
+                        "writing its rows to OUTPUT as JSON")
+    p.add_argument("--prefill-only", action="store_true")
+    p.add_argument("--linear-rows", type=int, nargs="+")
+    p.add_argument("--linear-shape", dest="linear_shapes", type=int, nargs=2, action="append")
+    p.add_argument("--fused-schedule", type=int, choices=range(7), default=0)
+    p.add_argument("--fused-only", action="store_true")
+    p.add_argument("--fused-paired", action="store_true")
+    p.add_argument("--fused-schedules", type=int, nargs="+", choices=range(7),
+                   default=list(range(7)))
     return p.parse_args()
 
 
@@ -496,6 +512,176 @@ def phase_profile(torch, ops, xs, ws, sw, codes, sa, out, reps: int = 6) -> tupl
     return "\n".join(lines), exact
 
 
+# (N, K) of the reference microbenchmark's linear layers (benchmarks/microbench.py:175-188):
+# GDN QKVZ, full-attention QKV, MLP gate/up, MLP down, attention output and MTP fusion, each
+# at a two-way pipeline split and a two-way tensor split.
+LINEAR_SHAPES = [(16384, 5120), (8192, 5120), (14336, 5120), (7168, 5120), (34816, 5120),
+                 (17408, 5120), (5120, 17408), (5120, 8704), (5120, 6144), (5120, 3072),
+                 (5120, 10240), (2560, 10240)]
+
+
+def graph_time_us(torch, call, repeats=7, launches=100) -> dict:
+    """Per-call time of `call` as benchmarks/microbench.py:15-38 takes it: five eager calls,
+    `launches` calls captured in one graph, `repeats` event-timed replays; median, min and
+    max in us."""
+    for _ in range(5):
+        call()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(launches):
+            call()
+    times = []
+    for _ in range(repeats):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        end.record()
+        end.synchronize()
+        times.append(start.elapsed_time(end) * 1e3 / launches)
+    del graph
+    return {"median_us": round(statistics.median(times), 3), "min_us": round(min(times), 3),
+            "max_us": round(max(times), 3)}
+
+
+def linear_sweep(torch, ops, args) -> int:
+    """The reference microbenchmark's linear mode (benchmarks/microbench.py:172-361) on this
+    build's ops, without its vLLM lines (allspark_w8a16_gemm and allspark_repack_weight are
+    vLLM's, which this build does not carry). For each (N, K) of LINEAR_SHAPES (or
+    --linear-shape) and each row count M (--linear-rows; 1, 2, 4, 16, 256, 1024, or 256 and
+    1024 with --prefill-only):
+      * --fused-only (microbench.py:205-252): quantize_rows once, then each schedule of
+        --fused-schedules, checked bit for bit against schedule 0 before it is timed (and
+        here also after its graph replays), timed alone; --fused-paired adds three
+        baseline / candidate / baseline triples of schedule 0 against it.
+      * otherwise (:254-358): quantize + cutlass_channel_mm into the INT32 workspace and
+        quantize + fused_channel_mm (--fused-schedule), checked bit-equal (:298-301) and
+        timed, with quantize + channel_mm on the biased UINT8 codes (native_w8a8, not with
+        --prefill-only), the AllSpark restore followed by each of the two (M >= 256) and
+        channel_gemv (M <= 8).
+    Weights are BF16 randn * 0.01 encoded by quantize_channel (the reference's per-channel
+    encoder), activations BF16 randn, both from torch's generator seeded as microbench.py:75
+    seeds it. The restore lines read random bytes of the packed shape (its packer is vLLM's)
+    and write buffers of their own, so they time the same work on other weights. Every row
+    is printed and the whole table rewritten to OUTPUT as it grows; a schedule whose output
+    differs is recorded with `"exact": false`, not timed, and makes the exit status 1."""
+    from consumer_int8.quantization import quantize_channel
+
+    torch.manual_seed(20261011)
+    results = {"gpu": torch.cuda.get_device_name(), "torch": torch.__version__,
+               "device": {"cus": torch.cuda.get_device_properties(0).multi_processor_count},
+               "rows": []}
+    shapes = [tuple(s) for s in args.linear_shapes] if args.linear_shapes else LINEAR_SHAPES
+    row_counts = args.linear_rows or ((256, 1024) if args.prefill_only else (1, 2, 4, 16, 256, 1024))
+    output = Path(args.linear_sweep)
+    output.parent.mkdir(parents=True, exist_ok=True)
+    failed = False
+
+    def record(row):
+        results["rows"].append(row)
+        output.write_text(json.dumps(results, indent=2))
+        print(json.dumps(row), flush=True)
+
+    def same_bits(x, y):
+        return bool(torch.equal(x.view(torch.int16), y.view(torch.int16)))
+
+    for n, k in shapes:
+        weight = torch.randn(n, k, device="cuda", dtype=torch.bfloat16) * 0.01
+        codes, scale = quantize_channel(weight)
+        signed = (codes.to(torch.int16) - 128).to(torch.int8)
+        del weight
+        padded_n = (n + 31) // 32 * 32
+        packed = torch.randint(0, 256, (padded_n, k), device="cuda", dtype=torch.uint8)
+        packed_scale = (torch.rand(padded_n, device="cuda") * 1e-3).to(torch.bfloat16)
+        restored = torch.empty(n, k, device="cuda", dtype=torch.int8)
+        restored_scale = torch.empty(n, device="cuda", dtype=torch.bfloat16)
+        for m in row_counts:
+            x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+            a = torch.empty_like(x, dtype=torch.int8)
+            sa = torch.empty(m, device="cuda")
+            out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+            workspace = torch.empty(m, n, device="cuda", dtype=torch.int32)
+            if args.fused_only:
+                ops.quantize_rows(x, a, sa)
+                ops.fused_channel_mm(a, signed, sa, scale, out, 0)
+                expected = out.clone()
+                for schedule in args.fused_schedules:
+                    def call(schedule=schedule):
+                        ops.fused_channel_mm(a, signed, sa, scale, out, schedule)
+
+                    call()
+                    row = {"op": "fused_channel_mm", "m": m, "n": n, "k": k, "schedule": schedule}
+                    if not same_bits(out, expected):
+                        failed = True
+                        record({**row, "exact": False})
+                        continue
+                    timing = graph_time_us(torch, call, repeats=5, launches=10)
+                    pairs = []
+                    if args.fused_paired:
+                        def baseline():
+                            ops.fused_channel_mm(a, signed, sa, scale, out, 0)
+
+                        for _ in range(3):
+                            before = graph_time_us(torch, baseline, 3, 20)["median_us"]
+                            candidate = graph_time_us(torch, call, 3, 20)["median_us"]
+                            after = graph_time_us(torch, baseline, 3, 20)["median_us"]
+                            pairs.append({"before_us": before, "candidate_us": candidate,
+                                          "after_us": after,
+                                          "speedup": round((before + after) / 2 / candidate, 4)})
+                    exact = same_bits(out, expected)
+                    failed |= not exact
+                    record({**row, "exact": exact, "paired": pairs, **timing,
+                            "tflops": round(2 * m * n * k / (timing["median_us"] * 1e6), 2)})
+                del expected, x, a, sa, out, workspace
+                continue
+
+            def quantized(gemm, *operands):
+                ops.quantize_rows(x, a, sa)
+                gemm(a, *operands)
+
+            def cutlass():
+                quantized(ops.cutlass_channel_mm, signed, sa, scale, workspace, out)
+
+            def fused():
+                quantized(ops.fused_channel_mm, signed, sa, scale, out, args.fused_schedule)
+
+            cutlass()
+            expected = out.clone()
+            fused()
+            row = {"op": "linear", "m": m, "n": n, "k": k, "fused_schedule": args.fused_schedule}
+            if not same_bits(out, expected):
+                failed = True
+                record({**row, "fused_matches_separate_exactly": False})
+                del expected, x, a, sa, out, workspace
+                continue
+            if not args.prefill_only:
+                row["native_w8a8"] = graph_time_us(
+                    torch, lambda: quantized(ops.channel_mm, codes, sa, scale, out))
+            row["cutlass_w8a8"] = graph_time_us(torch, cutlass)
+            row["fused_w8a8"] = graph_time_us(torch, fused)
+            row["fused_matches_separate_exactly"] = same_bits(out, expected)
+            failed |= not row["fused_matches_separate_exactly"]
+            if m >= 256:
+                def restore():
+                    ops.unpack_allspark(packed, packed_scale, restored, restored_scale)
+
+                row["unpack_fused_w8a8"] = graph_time_us(torch, lambda: (
+                    restore(), quantized(ops.fused_channel_mm, restored, sa, restored_scale,
+                                         out, args.fused_schedule)))
+                row["unpack_cutlass_w8a8"] = graph_time_us(torch, lambda: (
+                    restore(), quantized(ops.cutlass_channel_mm, restored, sa, restored_scale,
+                                         workspace, out)))
+            if m <= 8:
+                row["canonical_gemv_w8a16"] = graph_time_us(
+                    torch, lambda: ops.channel_gemv(x, signed, scale, out))
+            row["fused_tops"] = round(2 * m * n * k / (row["fused_w8a8"]["median_us"] * 1e6), 2)
+            record(row)
+            del expected, x, a, sa, out, workspace
+        del codes, scale, signed, packed, packed_scale, restored, restored_scale
+        torch.cuda.empty_cache()
+    return 1 if failed else 0
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -512,6 +698,8 @@ def main() -> int:
     props = torch.cuda.get_device_properties(0)
     cus = props.multi_processor_count
     peak_tops = PEAK_INT8_TOPS * cus / 256
+    if args.linear_sweep:
+        return linear_sweep(torch, ops, args)
     host, xs, ws, sw, codes, sa, out = make_inputs(torch)
     if args.phase_profile:
         table, exact = phase_profile(torch, ops, xs, ws, sw, codes, sa, out)
