@@ -1231,18 +1231,21 @@ using WLds256 = WLdsConfig<256, 8, false>;            // 4 waves, 64x256 per wav
 // 256-wide and persistent kernels.
 static_assert(WLds256::BN == kPlanWideBN && WLds224::BN == kPlanBN, "tile_plan.h widths");
 
-// Largest M the small-M kernel (gemm_small.hip) takes under schedule 0.
-constexpr int kSmallMaxM = 256;
-
 template <WeightCode kCode, bool kWorkspace>
 hipError_t dispatch(const int8_t* a, const void* w, const float* sa, const void* sw, void* out,
                     int32_t* ws, int m, int n, int k, int schedule, hipStream_t stream) {
   const int cus = device_cu_count();
-  if (schedule == 0 && m <= kSmallMaxM)
-    return launch_small_m_gemm(a, w, kCode, sa, sw, out, ws, m, n, k, cus > 0 ? cus : 256,
-                               stream);
   int choice = schedule;
-  if (choice == 0) choice = m < 1024 ? 1 : (wide_tiles_pay(m, n, cus) ? 3 : 4);
+  // Schedule 0 up to M = kSmallMaxM (tile_plan.h): the small-M kernel (gemm_small.hip), or
+  // above kSmallOnlyMaxM 128 x 128 or 256 x 224 tiles where they finish sooner.
+  if (schedule == 0 && m <= kSmallMaxM) {
+    choice = mid_m_schedule(m, n, cus);
+    if (choice == 0)
+      return launch_small_m_gemm(a, w, kCode, sa, sw, out, ws, m, n, k, cus > 0 ? cus : 256,
+                                 stream);
+  }
+  if (choice == 0)
+    choice = m < 1024 || medium_tiles_pay(m, n, cus) ? 1 : (wide_tiles_pay(m, n, cus) ? 3 : 4);
   // Without the INT32 copy, M >= 1024: the persistent two-waves-per-SIMD kernel
   // (gemm_pp.hip) for either weight code (its epilogue reads the channel scales 8 bytes
   // at a time) in place of the 224-wide one, and also in place of the 256-wide one
@@ -1250,8 +1253,8 @@ hipError_t dispatch(const int8_t* a, const void* w, const float* sa, const void*
   // M = 16384, K = 17408, N = 5120: 5 rounds of 224-wide tiles and one of 160-wide beat 5
   // rounds of 256-wide; M = N = 4096: 2 rounds lose to 1).
   if constexpr (!kWorkspace) {
-    if (schedule == 0 && m >= 1024 && n % 4 == 0 && reinterpret_cast<uintptr_t>(sw) % 8 == 0 &&
-        (choice == 4 || pp_beats_wide_tiles(m, n, cus)))
+    if (schedule == 0 && m >= 1024 && choice != 1 && n % 4 == 0 &&
+        reinterpret_cast<uintptr_t>(sw) % 8 == 0 && (choice == 4 || pp_beats_wide_tiles(m, n, cus)))
       return launch_pp_gemm(a, w, kCode, sa, sw, out, m, n, k, stream);
   }
   switch (choice) {

@@ -261,28 +261,13 @@ hipError_t run_small(const int8_t* a, const void* w, const float* sa, const void
   return hipGetLastError();
 }
 
-// Tile shapes, as (BM, BN). A launch runs its tiles in rounds of one per CU, and a
-// round lasts about as long as one tile takes to stream its (BM + BN) x K operand
-// bytes, so the cost of a shape is rounds x (BM + BN); ties go to the larger tile.
-struct Shape {
-  int bm, bn;
-};
-constexpr Shape kShapes[] = {{64, 32}, {32, 64}, {16, 64}, {32, 32}, {32, 16}, {16, 32}, {16, 16}};
-
-int64_t shape_cost(Shape s, int m, int n, int cus) {
-  const int64_t tiles = int64_t((m + s.bm - 1) / s.bm) * ((n + s.bn - 1) / s.bn);
-  return (tiles + cus - 1) / cus * (s.bm + s.bn);
-}
-
 }  // namespace
 
 template <WeightCode kCode, bool kWorkspace>
 hipError_t launch_small_m_gemm_t(const int8_t* a, const void* w, const float* sa, const void* sw,
                                  void* out, int32_t* ws, int m, int n, int k, int cus,
                                  hipStream_t stream) {
-  Shape best = kShapes[0];
-  for (const Shape s : kShapes)
-    if (shape_cost(s, m, n, cus) < shape_cost(best, m, n, cus)) best = s;
+  const SmallShape best = small_best_shape(m, n, cus);
 #define CI8_SMALL(BM_, BN_)                                                                  \
   if (best.bm == BM_ && best.bn == BN_)                                                      \
     return run_small<SmallConfig<BM_, BN_>, kCode, kWorkspace>(a, w, sa, sw, out, ws, m, n, \

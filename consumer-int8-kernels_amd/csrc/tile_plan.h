@@ -80,4 +80,77 @@ inline bool pp_beats_wide_tiles(int m, int n, int cus) {
   return pp_plan(m, n, cus).cost * 6 <= rounds256 * kPlanWideBN * 7;
 }
 
+// Tile shapes of the small-M kernel (gemm_small.hip), as (BM, BN). A launch runs its tiles
+// in rounds of one per CU, and a round lasts about as long as one tile takes to stream its
+// (BM + BN) x K operand bytes, so the cost of a shape is rounds x (BM + BN); ties go to the
+// larger tile (the earlier entry).
+struct SmallShape {
+  int bm, bn;
+};
+constexpr SmallShape kSmallShapes[] = {{64, 32}, {32, 64}, {16, 64}, {32, 32},
+                                       {32, 16}, {16, 32}, {16, 16}};
+
+inline int64_t small_shape_cost(SmallShape s, int m, int n, int cus) {
+  const int64_t tiles = int64_t((m + s.bm - 1) / s.bm) * ((n + s.bn - 1) / s.bn);
+  return (tiles + cus - 1) / cus * (s.bm + s.bn);
+}
+
+inline SmallShape small_best_shape(int m, int n, int cus) {
+  SmallShape best = kSmallShapes[0];
+  for (const SmallShape s : kSmallShapes)
+    if (small_shape_cost(s, m, n, cus) < small_shape_cost(best, m, n, cus)) best = s;
+  return best;
+}
+
+// Largest M the small-M kernel takes under schedule 0, and the M above which it competes
+// with the 128 x 128 and 256 x 224 kernels (mid_m_schedule).
+constexpr int kSmallMaxM = 256, kSmallOnlyMaxM = 128;
+
+// Schedule 0 for kSmallOnlyMaxM < M <= kSmallMaxM: 0 (the small-M kernel), 1 (128 x 128
+// tiles) or 4 (256 x 224 tiles), whichever a time model of the three finishes first. The
+// model's figures are per-launch times measured on MI355X at K = 5120 (each kernel's time
+// is proportional to K, so the comparison holds at any K), conditioned graph replays,
+// identical outputs:
+//   small-M:  (its shape cost) / 13.3 us (M = 256, 64 x 32 tiles: 4 / 8 / 17 rounds took
+//             29.7 / 57.3 / 119.2 us at N = 8192 / 16384 / 34816);
+//   128x128:  35.5 us while its tiles fit one round (34.6-36.4 us from 80 to 256 tiles);
+//             past that, whole rounds plus the rest's share of a round but at least 0.37
+//             of one, as two workgroups fit a CU (M = 256: 272 / 384 / 544 tiles took
+//             48.5 / 53.2 / 86.8 us);
+//   256x224:  60 us a round (57.1-61.0 us from 23 to 156 tiles).
+// At M = 256 this takes N = 11264-24576 from 43.4-85.0 us to 34.9-53.2 us and N = 34816
+// from 119.2 to 60.3 us, and keeps the small-M kernel up to N = 8192, where it is fastest
+// (160 <= M <= 256, N from 5120 to 34816, K = 2048-17408). M <= kSmallOnlyMaxM keeps the
+// small-M kernel: its rows fill every tile of the other two, and streaming the weights
+// bounds all three alike.
+inline int mid_m_schedule(int m, int n, int cus) {
+  if (cus <= 0 || m <= kSmallOnlyMaxM || m > kSmallMaxM) return 0;
+  const double small = double(small_shape_cost(small_best_shape(m, n, cus), m, n, cus)) / 13.3;
+  const int64_t tiles128 = int64_t((m + 127) / 128) * ((n + 127) / 128);
+  double rounds128 = 1.0;
+  if (tiles128 > cus) {
+    const int64_t rest = tiles128 % cus;
+    rounds128 = double(tiles128 / cus);
+    if (rest > 0) rounds128 += rest * 100 > cus * 37 ? double(rest) / cus : 0.37;
+  }
+  const double medium = 35.5 * rounds128;
+  const int64_t tiles224 = int64_t((m + kPlanBM - 1) / kPlanBM) * ((n + kPlanBN - 1) / kPlanBN);
+  const double wide = 60.0 * double((tiles224 + cus - 1) / cus);
+  if (small <= medium && small <= wide) return 0;
+  return medium <= wide ? 1 : 4;
+}
+
+// Whether 128 x 128 tiles beat the persistent kernel at M >= 1024: when its 256 x 224 tiles
+// would keep under half the CUs busy and 128 x 128 tiles fit in one round (measured on
+// MI355X, conditioned graph replays, identical outputs: M = 1024, N = 2560 / 3072 / 2048,
+// K = 10240 / 5120 / 8192: 63.5 / 35.0 / 51.6 against 76.7 / 43.8 / 62.0 us; with more than
+// one round of 128 x 128 tiles it is not faster: M = 1024, N = 5120, K = 10240: 81.0
+// against 77.3 us, M = 2048, N = 2560: 44.4 against 44.7 us).
+inline bool medium_tiles_pay(int m, int n, int cus) {
+  if (cus <= 0 || m < 1024) return false;
+  const int64_t tiles224 = int64_t((m + kPlanBM - 1) / kPlanBM) * ((n + kPlanBN - 1) / kPlanBN);
+  const int64_t tiles128 = int64_t((m + 127) / 128) * ((n + 127) / 128);
+  return 2 * tiles224 < cus && tiles128 <= cus;
+}
+
 }  // namespace ci8

@@ -309,6 +309,46 @@ def test_persistent_tile_switches(ops, m, n, k, biased):
     full_size_check(a_np, w_signed, sa_np, sw_np, acc, out_bits, samples=8)
 
 
+@pytest.mark.parametrize("m,n,k,biased", [
+    # 128 < M <= 256 on 256 CUs (tests/test_tile_plan.py checks the choices): 128 x 128
+    # tiles in one round, in 1.5 rounds with a K tail, and at M = 160; 256 x 224 tiles.
+    (256, 11264, 256, False),
+    (256, 24576, 160, False),
+    (160, 16384, 96, True),
+    (200, 34816, 128, True),
+    # M >= 1024 with under half the CUs' worth of persistent tiles: 128 x 128 tiles.
+    (1024, 2560, 544, True),
+    (1100, 2000, 256, False),
+])
+def test_schedule0_mid_m_and_few_tile_choices(ops, m, n, k, biased):
+    """Schedule 0 where it runs the 128 x 128 or the 256 x 224 kernel in place of the
+    small-M or the persistent kernel. The output equals the 256 x 32 tiling's (schedule 5)
+    and that of the workspace op (which takes the same choice), whose exact INT32
+    accumulators are checked against the oracle through checksums and sampled rows and
+    columns."""
+    rng = np.random.default_rng(m * 7 + n + k + biased)
+    a_np, w_np, sa_np, sw_np = gemm_inputs(rng, m, n, k, biased=biased)
+    w_signed = O.debias(w_np) if biased else w_np
+    a, sa, sw, ws_dev = to_dev(a_np), to_dev(sa_np), to_dev(sw_np), to_dev(w_signed)
+    out, buf = with_guard((m, n), torch.bfloat16, float("nan"))
+    print(f"schedule 0 choice m={m} n={n} k={k} biased={biased}", flush=True)
+    if biased:
+        ops.channel_mm(a, to_dev(w_np), sa, sw, out)
+    else:
+        ops.fused_channel_mm(a, ws_dev, sa, sw, out, 0)
+    ref = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    ops.fused_channel_mm(a, ws_dev, sa, sw, ref, 5)
+    acc = torch.empty(m, n, device="cuda", dtype=torch.int32)
+    out2 = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    ops.cutlass_channel_mm(a, ws_dev, sa, sw, acc, out2)
+    torch.cuda.synchronize()
+    out_bits = bf16_bits(out)
+    assert guard_intact(buf, float("nan"))
+    assert np.array_equal(out_bits, bf16_bits(ref))
+    assert np.array_equal(out_bits, bf16_bits(out2))
+    full_size_check(a_np, w_signed, sa_np, sw_np, acc, out_bits, samples=8)
+
+
 @pytest.mark.parametrize("biased", [False, True])
 def test_column_split_in_graph_replays(ops, biased):
     """The column split (a launch of 224-wide tiles over whole rounds, then one of
