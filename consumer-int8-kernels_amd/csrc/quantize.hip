@@ -14,7 +14,7 @@
 // at most a few 16-byte packs; eight when a few rows of 2,561..4,096 values leave most
 // CUs idle) and keep it in registers between the max reduction and the
 // store, so HBM sees a single read of x and a single write of the codes, with 16-byte
-// loads and 8-byte nontemporal stores fully coalesced across the wave.
+// loads and 8-byte stores (nontemporal outside 256..1,024 rows) fully coalesced across the wave.
 #include "ci8_device.h"
 #include "launch.h"
 
@@ -33,7 +33,7 @@ __device__ __forceinline__ float wave_max(float v) {
 // kWaves waves cooperate on one row when kWaves > 1 (very wide rows).
 // Grouped: output row o reads input row (o % m) * groups + o / m ([m,g,k] -> [g,m,k]).
 // Workgroups hold four waves (1, 2 or 4 rows), or kWaves waves and one row for kWaves > 4.
-template <int kPacks, int kWaves, bool kGrouped, bool kNt>
+template <int kPacks, int kWaves, bool kGrouped, int kPolicy>
 __global__ void __launch_bounds__(kWaves > 4 ? 64 * kWaves : 256) quantize_rows_vec_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ codes, float* __restrict__ scales,
     int rows, int k, int m, int groups) {
@@ -53,7 +53,7 @@ __global__ void __launch_bounds__(kWaves > 4 ? 64 * kWaves : 256) quantize_rows_
   for (int i = 0; i < kPacks; ++i) {
     const int col = ((i * kWaves + part) * kWave + lane) * 8;
     packed[i] = u32x4{0, 0, 0, 0};
-    if (active && col < k) packed[i] = load16<kNt>(src + col);
+    if (active && col < k) packed[i] = load16<(kPolicy == 2)>(src + col);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t word = packed[i][j];
@@ -79,8 +79,13 @@ __global__ void __launch_bounds__(kWaves > 4 ? 64 * kWaves : 256) quantize_rows_
 #pragma unroll
   for (int i = 0; i < kPacks; ++i) {
     const int col = ((i * kWaves + part) * kWave + lane) * 8;
-    if (col < k)  // codes are not re-read by this kernel: stream them past the caches
-      __builtin_nontemporal_store(codes8(packed[i], scale, inv), reinterpret_cast<u32x2*>(dst + col));
+    if (col < k) {
+      const u32x2 code = codes8(packed[i], scale, inv);
+      if constexpr (kPolicy >= 1)
+        __builtin_nontemporal_store(code, reinterpret_cast<u32x2*>(dst + col));
+      else
+        *reinterpret_cast<u32x2*>(dst + col) = code;
+    }
   }
 }
 
@@ -113,16 +118,30 @@ hipError_t dispatch(const void* x, int8_t* codes, float* scales, int rows, int k
   const int packs = (k + 511) / 512;  // 16-byte packs per lane with one wave per row
   // Inputs past the MALL's size are read with nontemporal loads (kMallBytes).
   const bool nt = int64_t(rows) * k * 2 > kMallBytes;
+  // Codes are stored nontemporally (past the caches) except for 256 to 1,024 rows. There the
+  // GEMM that reads them next runs faster when they stay cached (measured on MI355X, graph
+  // replays of quantize_rows + fused_channel_mm, identical outputs). At M = 1024, N = 5120
+  // and K = 5120 / 8704 / 17408 the pair took 52.8 / 75.6 / 136.0 us against 59.0 / 86.3 /
+  // 153.9 us, and M = 256, N = 5120, K = 17408 took 66.7 against 70.0 us. The quantizer alone
+  // is faster with nontemporal stores ([1024, 17408]: 11.3 against 13.7 us). At 4,096 rows
+  // ([4096, 5120], N = 5120) the pair gained only 1.4 us against a 0.6 us slower quantizer,
+  // so larger inputs keep them, and so do fewer rows, whose GEMM is latency-bound.
+  // Policy (a template argument, so the store loop has no branch): 0 plain loads and
+  // stores, 1 nontemporal stores, 2 nontemporal loads and stores.
+  const int policy = nt ? 2 : (rows >= 256 && rows <= 1024 ? 0 : 1);
 #define CI8_QW(W, P)                                                                       \
   if (packs <= (W) * (P)) {                                                                \
     constexpr int kPerBlock = (W) > 4 ? 1 : 4 / (W);                                       \
     constexpr int kThreads = (W) > 4 ? 64 * (W) : 256;                                     \
     const int blocks = (rows + kPerBlock - 1) / kPerBlock;                                 \
-    if (nt)                                                                                \
-      quantize_rows_vec_kernel<P, W, kGrouped, true><<<blocks, kThreads, 0, stream>>>(      \
+    if (policy == 2)                                                                       \
+      quantize_rows_vec_kernel<P, W, kGrouped, 2><<<blocks, kThreads, 0, stream>>>(         \
+          src, codes, scales, rows, k, m, groups);                                         \
+    else if (policy == 1)                                                                  \
+      quantize_rows_vec_kernel<P, W, kGrouped, 1><<<blocks, kThreads, 0, stream>>>(         \
           src, codes, scales, rows, k, m, groups);                                         \
     else                                                                                   \
-      quantize_rows_vec_kernel<P, W, kGrouped, false><<<blocks, kThreads, 0, stream>>>(     \
+      quantize_rows_vec_kernel<P, W, kGrouped, 0><<<blocks, kThreads, 0, stream>>>(         \
           src, codes, scales, rows, k, m, groups);                                         \
     return hipGetLastError();                                                              \
   }
